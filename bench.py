@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the Prefill MoE layer on one MI355X.
+
+A step is one full layer call (router GEMM, top-k, grouping, gather, shared FFN, routed
+gate/up + SwiGLU, routed down, combine) over one chunk of synthetic tokens whose inputs
+are already resident in HBM. Default workload: configuration 2 (T=2048, d=2048, E=512,
+top-10, I=512, Q4_K gate/up, Q8_0 down, F16 shared expert with I=512).
+
+Prints ONE JSON line with whole-job tokens/s, per-stage microseconds, the roofline of the
+dominant kernel (the routed gate/up product) and the CPU baseline (the repo's C++
+restatement of the same stages, timed on a bounded sample of the same workload).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, help="configuration index (0-4)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
+              f"multi-GPU path — run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__ as ge
+
+    pkg = ge.load_package()
+    moe, layer = pkg.moe, pkg.layer
+    cfg = layer.CONFIGS[args.config]
+    T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
+    N = T * K
+    log(f"config {args.config} ({cfg.name}): generating inputs")
+    t0 = time.time()
+    inp = layer.make_inputs(cfg)
+    log(f"inputs ready in {time.time() - t0:.1f}s; uploading")
+    ctx = moe.Context(0)
+    chunks = [layer.LayerWorkspace(ctx, cfg, inp, chunk=c) for c in range(cfg.chunks)]
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    # Pre-encoded buffer structs: the timed loop encodes + validates + commits each step.
+    lbs = [ws.layer_buffers() for ws in chunks]
+
+    def step():
+        for ws, lb in zip(chunks, lbs):
+            seg = ctx.segment()
+            ok, err = seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, lb)
+            if not ok:
+                seg.abort()
+                raise RuntimeError(err)
+            seg.commit(sh)
+
+    log("warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    for ws in chunks:
+        st = ws.read_status(sh)
+        if st != (0, 0, 0):
+            raise RuntimeError(f"layer status {st}")
+    log(f"timing {args.steps} steps")
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    tokens_per_step = T * cfg.chunks
+    value = tokens_per_step / (ms_per_step / 1e3)
+    log(f"{ms_per_step:.3f} ms/step, {value:,.0f} tokens/s (wall {wall:.3f}s)")
+
+    # ---- per-stage timing (each stage as its own segment, repeated back to back) ----
+    ws = chunks[0]
+    reps = max(5, args.steps)
+
+    def stage_ms(encode):
+        for _ in range(2):
+            s = ctx.segment(); ok, err = encode(s); assert ok, err; s.commit(sh)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            s = ctx.segment(); ok, err = encode(s); assert ok, err; s.commit(sh)
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    rg, gub, dnb, cob = ws.route_gather_buffers(), ws.gate_up_buffers(), ws.down_buffers(), ws.combine_buffers()
+    shb = ws.shared_buffers()
+    rb, gb = ws.route_buffers(), ws.grouping_buffers()
+    stages = {}
+    stages["route_gather"] = stage_ms(lambda s: s.encode_prefill_moe_full_mode_route_gather(ws.shape, rg))
+    stages["top_k"] = stage_ms(lambda s: s.encode_moe_route(ws.shape, True, rb))
+    stages["grouping_gather"] = stage_ms(lambda s: s.encode_prefill_moe_grouping(ws.shape, gb))
+    if Is:
+        stages["shared_ffn"] = stage_ms(lambda s: s.encode_prefill_moe_shared_ffn(ws.shape, cfg.shared_fmt, shb))
+    stages["gate_up"] = stage_ms(lambda s: s.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, gub))
+    stages["down"] = stage_ms(lambda s: s.encode_prefill_moe_down(ws.shape, cfg.down_fmt, dnb))
+    stages["combine"] = stage_ms(lambda s: s.encode_prefill_moe_combine(ws.shape, cob))
+    stage_us = {k: round(v * 1e3, 2) for k, v in stages.items()}
+    log(f"stages (us): {stage_us}")
+
+    # ---- roofline of the dominant kernel: routed gate/up ----
+    plan = ws.plan.tensor.cpu().numpy().view(np.uint32)
+    n_groups = int(plan[0])
+    gu_row = moe.row_bytes(cfg.gate_up_fmt, d)
+    dn_row = moe.row_bytes(cfg.down_fmt, I)
+    gu_bytes = n_groups * 2 * I * gu_row + N * d * 2 + N * I * 2
+    gu_flops = 2.0 * N * 2 * I * d
+    gu_s = stages["gate_up"] / 1e3
+    gu_gbs = gu_bytes / gu_s / 1e9
+    gu_tflops = gu_flops / gu_s / 1e12
+    dn_bytes = n_groups * d * dn_row + N * I * 2 + N * d * 4
+    ai = gu_flops / gu_bytes
+    bound = "mfma" if ai > F16_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu_gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(gu_tflops, 1), "peak": F16_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(gu_tflops / F16_MFMA_PEAK_TFLOPS, 4)}
+    roof.update({"kernel": "routed_gemm_kernel<gate/up>", "traffic": None,
+                 "algorithmic_bytes": gu_bytes, "algorithmic_flops": gu_flops,
+                 "tflops": round(gu_tflops, 1), "gbs": round(gu_gbs, 1)})
+    gather_bytes = N * d * 2 + T * d * 2 + N * 4
+    comb_bytes = N * d * 4 + N * 4 + (2 * T * d * 4 + T * 4 if Is else T * d * 4)
+    extra = {
+        "gather_combine_gbs": {
+            "grouping_gather": round(gather_bytes / (stages["grouping_gather"] / 1e3) / 1e9, 1),
+            "combine": round(comb_bytes / (stages["combine"] / 1e3) / 1e9, 1),
+        },
+        "down": {"us": stage_us["down"], "gbs": round(dn_bytes / (stages["down"] / 1e3) / 1e9, 1),
+                 "tflops": round(2.0 * N * d * I / (stages["down"] / 1e3) / 1e12, 1)},
+        "layer_tflops": round(layer.layer_flops(cfg) * cfg.chunks / (ms_per_step / 1e3) / 1e12, 1),
+    }
+
+    # ---- CPU baseline: the C++ restatement of the same stages on a bounded sample ----
+    cpu = None
+    if not args.no_cpu:
+        orc = ge.load_oracle()
+        log("cpu baseline")
+        _, st, threads = orc.cpu_layer(cfg, inp, n_threads=args.cpu_threads)  # warm-up
+        times = []
+        t_budget = time.time()
+        while len(times) < 3 and (time.time() - t_budget) < 30.0:
+            a = time.perf_counter()
+            orc.cpu_layer(cfg, inp, n_threads=args.cpu_threads)
+            times.append(time.perf_counter() - a)
+        med = sorted(times)[len(times) // 2]
+        cpu = {"value": round(T / med, 1), "unit": "tokens/s", "cores": int(threads), "kind": "port",
+               "sample": f"{len(times)} timed call(s) of one {T}-token chunk of configuration {args.config} "
+                         f"(all stages, median {med:.3f}s) after one warm-up call",
+               "stage_us": {k: round(float(v), 1) for k, v in zip(
+                   ["router", "top_k", "grouping_gather", "shared_ffn", "gate_up", "down", "combine"], st)}}
+        log(f"cpu baseline {cpu['value']} tokens/s on {threads} threads")
+
+    line = {
+        "metric": "MoE-layer prefill tokens/s",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) F16 activations, N(0,0.02) weights quantized in-repo)",
+        "config": {"workload": f"config{args.config}:{cfg.name}", "tokens": T * cfg.chunks, "hidden": d,
+                   "experts": E, "top_k": K, "expert_ff": I, "shared_ff": Is,
+                   "gate_up": moe.FORMAT_NAMES[cfg.gate_up_fmt], "down": moe.FORMAT_NAMES[cfg.down_fmt],
+                   "shared": moe.FORMAT_NAMES[cfg.shared_fmt] if Is else None, "chunks": cfg.chunks,
+                   "parallelism": "single-gpu"},
+        "stages_us": stage_us,
+        "roofline": roof,
+        "extra": extra,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

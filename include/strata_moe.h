@@ -1,0 +1,312 @@
+/*
+ * strata_moe.h — C ABI of the MI355X Prefill MoE layer (libstrata_moe.so).
+ *
+ * Drop-in boundary for the reference's Prefill MoE coordinators
+ * (namespace strata::metal in the reference checkout). Each reference coordinator has two
+ * forms; both are kept:
+ *   - a SEGMENT form: sm_encode_*(segment, ...) validates and records launches into an open
+ *     segment (the reference's caller-owned `Encoder&` overload). On failure it returns a
+ *     non-zero status, records the message, and poisons the segment: the caller must
+ *     propagate the failure and call sm_segment_abort(), exactly as the reference requires
+ *     callers to propagate `false` so the whole segment is discarded
+ *     (include/strata/metal/prefill_moe_full_pipeline.hpp:64-67).
+ *   - a STANDALONE form: sm_submit_*(context, stream, ..., err, err_cap) begins a segment,
+ *     encodes, then commits or aborts (the reference's `CommandBuffer&` overload,
+ *     prefill_moe_full_pipeline.hpp:75-82; encoder.mm:165-231).
+ * Nothing reaches the GPU unless every stage of the segment validated: launches are
+ * deferred until sm_segment_commit().
+ *
+ * Buffers are caller-owned device allocations registered with the context (the reference's
+ * "owned by this Context" check, context.hpp:405-413). A view is {buffer handle, byte
+ * offset, byte length} (the reference's BufferRef, context.hpp:136-233). The library never
+ * allocates device memory on the layer path.
+ *
+ * Status words (u32 in caller device memory) keep the reference's bits
+ * (prefill_moe_expert_dispatch.hpp:46-50): bit0 an active expert's weight address is null,
+ * bit1 the grouping plan / tile list / destination permutation is invalid. Failing tiles
+ * write zeros. The plan's `bad` field counts route ids outside [0, n_experts)
+ * (prefill_moe_grouping.hpp:40-41); callers check both after completion.
+ *
+ * No C++ exception crosses this ABI. All functions are thread-compatible: one segment is
+ * used by one thread at a time; distinct segments may be encoded concurrently.
+ */
+#ifndef STRATA_MOE_H
+#define STRATA_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SM_ABI_VERSION 1u
+
+/* Error classes; each maps onto a class of reference validation message
+ * (prefill_moe_grouping_dispatch.mm:84-254, prefill_moe_full_pipeline.cpp:451-475). */
+typedef enum sm_status {
+    SM_OK = 0,
+    SM_E_ARGUMENT = 1,  /* null pointer / unknown enum                                   */
+    SM_E_SHAPE = 2,     /* unsupported rows, experts, top-k or widths                       */
+    SM_E_VIEW = 3,      /* "view is undersized or misaligned"                              */
+    SM_E_OWNERSHIP = 4, /* "view is not owned by this context"                              */
+    SM_E_ALIAS = 5,     /* "<output> overlaps active <range>"                               */
+    SM_E_SEGMENT = 6,   /* segment already failed / committed                               */
+    SM_E_FORMAT = 7,    /* weight format not supported for this role                        */
+    SM_E_ADDRESS = 8,   /* expert weight address outside declared storage or misaligned    */
+    SM_E_DEVICE = 9     /* HIP runtime error                                                */
+} sm_status;
+
+/* Weight formats (ggml block layouts, third_party/ggml/ggml-common.h:252-338). */
+typedef enum sm_format {
+    SM_FMT_Q8_0 = 1, /* 34 B / 32 values: f16 d, int8 q[32]                                 */
+    SM_FMT_Q4_K = 2, /* 144 B / 256: f16 d, f16 dmin, scales[12], q[128]                   */
+    SM_FMT_Q2_K = 3, /* 84 B / 256: scales[16], q[64], f16 d, f16 dmin                     */
+    SM_FMT_F16 = 4,  /* shared expert only                                                  */
+    SM_FMT_BF16 = 5  /* shared expert only                                                  */
+} sm_format;
+
+typedef struct sm_context sm_context;
+typedef struct sm_segment sm_segment;
+
+/* A byte range of a registered device allocation; buffer == 0 is the null view. */
+typedef struct sm_view {
+    uint64_t buffer;
+    uint64_t offset;
+    uint64_t length;
+} sm_view;
+
+/* Layer geometry (the reference hard-codes d=2560, k=10, I=640; here they are parameters).
+ * rows: tokens T in this chunk (1..SM_MAX_ROWS); hidden: d (multiple of 256);
+ * n_experts: E (1..512); top_k: k (1..min(E,32)); expert_ff: I (multiple of 256 when the
+ * down weights are K-quants, else of 64); shared_ff: I_s (0 = no shared expert). */
+typedef struct sm_moe_shape {
+    uint32_t rows;
+    uint32_t hidden;
+    uint32_t n_experts;
+    uint32_t top_k;
+    uint32_t expert_ff;
+    uint32_t shared_ff;
+} sm_moe_shape;
+
+#define SM_MAX_ROWS 419430u       /* prefill.hpp:15 (kPrefillMaxShaderRows)               */
+#define SM_MAX_EXPERTS 512u       /* PfPlan arrays, prefill_moe.metal:23-33              */
+#define SM_MAX_TOP_K 32u
+#define SM_PLAN_BYTES 6180u       /* prefill_moe_grouping.hpp:18                          */
+#define SM_PLAN_SLOT_BYTES 6400u  /* prefill_moe_grouping.hpp:17                          */
+#define SM_COUNT_TILE 256u        /* grouping histogram tile, prefill_moe.metal:52        */
+#define SM_EXPERT_TILE 64u        /* entries per tile-list tile, prefill_moe.metal:171-173 */
+
+/* Scratch sizes a caller must provide (bytes), given the shape. */
+uint64_t sm_histogram_bytes(const sm_moe_shape* shape); /* ceil(T*k/256) * E * 4     */
+uint64_t sm_tiles_bytes(const sm_moe_shape* shape);     /* (ceil(T*k/64) + E) * 8    */
+uint64_t sm_format_row_bytes(sm_format fmt, uint64_t values);
+
+/* ---- context, buffers, segments -------------------------------------------------------- */
+sm_status sm_context_create(int device, sm_context** out);
+void sm_context_destroy(sm_context* ctx);
+/* Registers a device allocation [ptr, ptr+bytes); returns a non-zero handle. */
+sm_status sm_buffer_register(sm_context* ctx, void* device_ptr, uint64_t bytes, uint64_t* handle);
+sm_status sm_buffer_unregister(sm_context* ctx, uint64_t handle);
+
+sm_status sm_segment_begin(sm_context* ctx, sm_segment** out);
+/* Launches every recorded step in order on `hip_stream` (a hipStream_t; NULL = default
+ * stream) and frees the segment. Refused (and the segment freed) if any encode failed. */
+sm_status sm_segment_commit(sm_segment* seg, void* hip_stream);
+/* Discards every recorded step; nothing ran. Frees the segment. */
+void sm_segment_abort(sm_segment* seg);
+/* Message of the first failure recorded in the segment ("" if none). */
+const char* sm_segment_error(const sm_segment* seg);
+uint32_t sm_segment_launches(const sm_segment* seg);
+
+/* ---- stage buffers (mirror the reference's *Buffers structs) ---------------------------- */
+
+/* encode_moe_route (moe_dispatch.cpp:345-379, moe.metal:17-86): logits F32 [T,E] ->
+ * ids I32 [T,k], weights F32 [T,k]. */
+typedef struct sm_route_buffers {
+    sm_view logits;
+    sm_view ids;
+    sm_view weights;
+} sm_route_buffers;
+
+/* PrefillMoeGroupingBuffers (prefill_moe_grouping.hpp:21-39), full residency. */
+typedef struct sm_grouping_buffers {
+    sm_view ids;              /* I32 [T*k] route ids, token-major                         */
+    sm_view mixed_h;          /* F16 [T,d], 16-byte aligned                               */
+    sm_view histogram;        /* U32 [ceil(T*k/256)][E]                                   */
+    sm_view plan;             /* 6400-byte PfPlan slot                                    */
+    sm_view tiles;            /* U32x2 [ceil(T*k/64)+E] {group, first_entry}              */
+    sm_view source_rows;      /* I32 [T*k]: grouped entry -> token                        */
+    sm_view destination_rows; /* I32 [T*k]: grouped entry -> route index t*k+r            */
+    sm_view gathered_rows;    /* F16 [T*k,d]                                              */
+} sm_grouping_buffers;
+
+/* PrefillMoeRouteGatherBuffers (prefill_moe_pipeline.hpp:21-33): router GEMM + top-k +
+ * grouping + gather. The router is F32 weights [E,d] against F16 activations. */
+typedef struct sm_route_gather_buffers {
+    sm_view mixed_h;          /* F16 [T,d]                                                */
+    sm_view router_weights;   /* F32 [E,d]                                                */
+    sm_view logits;           /* F32 [T,E]                                                */
+    sm_view route_ids;        /* I32 [T,k]                                                */
+    sm_view route_weights;    /* F32 [T,k], divide mode                                   */
+    sm_view histogram;
+    sm_view plan;
+    sm_view tiles;
+    sm_view source_rows;
+    sm_view destination_rows;
+    sm_view gathered_rows;
+    sm_view router_bias;      /* F32 [E] added to the logits; null view = none            */
+} sm_route_gather_buffers;
+
+/* Routed expert weights: a host copy of the [E][3] device-address table (gate, up, down;
+ * 0 = missing) as the reference keeps per layer (prefill_moe_expert_dispatch.hpp:21-22),
+ * validated against the declared storage views (prefill_moe_expert_dispatch.mm:377-448)
+ * and copied at commit into `address_snapshot` (device, E*3*8 bytes) before the kernels. */
+typedef struct sm_expert_weights {
+    const uint64_t* addresses;
+    sm_view address_snapshot;
+    const sm_view* storage;
+    uint32_t n_storage;
+} sm_expert_weights;
+
+/* PrefillMoeExpertTileBuffers (prefill_moe_expert_dispatch.hpp:20-51). */
+typedef struct sm_gate_up_buffers {
+    sm_expert_weights weights;
+    sm_view gathered_rows;    /* F16 [T*k,d]                                              */
+    sm_view plan;
+    sm_view tiles;
+    sm_view hidden;           /* F16 [T*k,I] = half_sat(silu(x.Wg) * (x.Wu))              */
+    sm_view status;           /* U32, cleared on the GPU before use                       */
+} sm_gate_up_buffers;
+
+/* PrefillMoeDownTileBuffers (prefill_moe_down_dispatch.hpp:12-38). */
+typedef struct sm_down_buffers {
+    sm_expert_weights weights;
+    sm_view hidden;           /* F16 [T*k,I]                                              */
+    sm_view plan;
+    sm_view tiles;
+    sm_view destinations;     /* I32 [T*k]                                                */
+    sm_view parts;            /* F32 [T*k,d] in route order                               */
+    sm_view status;           /* U32, distinct from the gate/up status                    */
+} sm_down_buffers;
+
+/* PrefillMoeSharedFFNBuffers (prefill_moe_shared_pipeline.hpp:29-42). The gate/up SwiGLU is
+ * fused into the projection epilogue, so no F32 gate/up or dequant scratch is needed. */
+typedef struct sm_shared_buffers {
+    sm_view mixed_h;          /* F16 [T,d]                                                */
+    sm_view gate_weights;     /* [I_s][d] in the shared format                            */
+    sm_view up_weights;       /* [I_s][d]                                                 */
+    sm_view down_weights;     /* [d][I_s]                                                 */
+    sm_view gate_vector;      /* [d] sigmoid-gate weights, shared format                  */
+    sm_view hidden;           /* F16 [T,I_s]                                              */
+    sm_view output;           /* F32 [T,d]                                                */
+    sm_view gate_logit;       /* F32 [T]                                                  */
+} sm_shared_buffers;
+
+/* PrefillMoeSwiGLUBuffers / PrefillMoeCombineBuffers (prefill_moe_post.hpp:15-27). */
+typedef struct sm_swiglu_buffers {
+    sm_view gate;             /* F32 [rows*width]                                         */
+    sm_view up;
+    sm_view output;           /* F16                                                      */
+} sm_swiglu_buffers;
+
+typedef struct sm_combine_buffers {
+    sm_view parts;            /* F32 [T,k,d]                                              */
+    sm_view weights;          /* F32 [T,k]                                                */
+    sm_view shared;           /* F32 [T,d]; null view when shared_ff == 0                 */
+    sm_view gate;             /* F32 [T];   null view when shared_ff == 0                 */
+    sm_view output;           /* F32 [T,d]                                                */
+} sm_combine_buffers;
+
+typedef struct sm_layer_formats {
+    sm_format gate_up;        /* Q8_0, Q4_K, Q2_K                                          */
+    sm_format down;           /* Q8_0, Q4_K, Q2_K                                          */
+    sm_format shared;         /* F16, BF16 (ignored when shared_ff == 0)                   */
+} sm_layer_formats;
+
+/* PrefillMoeFullPipelineBuffers (prefill_moe_full_pipeline.hpp:43-56). */
+typedef struct sm_layer_buffers {
+    sm_route_gather_buffers route_gather;
+    sm_shared_buffers shared;
+    sm_gate_up_buffers gate_up;
+    sm_down_buffers down;
+    sm_combine_buffers combine;
+} sm_layer_buffers;
+
+/* ---- coordinators: segment form ------------------------------------------------------- */
+/* encode_moe_route(divide_weights) — moe_dispatch.cpp:1500-1518. */
+sm_status sm_encode_route(sm_segment* seg, const sm_moe_shape* shape, int divide_weights,
+                          const sm_route_buffers* b);
+/* encode_prefill_moe_grouping — prefill_moe_grouping.hpp:50-53. */
+sm_status sm_encode_grouping(sm_segment* seg, const sm_moe_shape* shape,
+                             const sm_grouping_buffers* b);
+/* encode_prefill_moe_full_mode_route_gather — prefill_moe_pipeline.hpp:51-55. */
+sm_status sm_encode_route_gather(sm_segment* seg, const sm_moe_shape* shape,
+                                 const sm_route_gather_buffers* b);
+/* encode_prefill_moe_shared_ffn — prefill_moe_shared_pipeline.hpp:54-58. */
+sm_status sm_encode_shared_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                               const sm_shared_buffers* b);
+/* encode_prefill_moe_gu_<fmt> — prefill_moe_expert_dispatch.hpp:55-99. */
+sm_status sm_encode_gate_up(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                            const sm_gate_up_buffers* b);
+/* encode_prefill_moe_down_<fmt> — prefill_moe_down_dispatch.hpp:40-49. */
+sm_status sm_encode_down(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                         const sm_down_buffers* b);
+/* encode_prefill_moe_swiglu — prefill_moe_post.hpp:31-34. */
+sm_status sm_encode_swiglu(sm_segment* seg, uint32_t rows, uint32_t width,
+                           const sm_swiglu_buffers* b);
+/* encode_prefill_moe_combine — prefill_moe_post.hpp:46-49. */
+sm_status sm_encode_combine(sm_segment* seg, const sm_moe_shape* shape,
+                            const sm_combine_buffers* b);
+/* encode_prefill_moe_full_mode_layer — prefill_moe_full_pipeline.hpp:68-73. */
+sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape,
+                               const sm_layer_formats* formats, const sm_layer_buffers* b);
+
+/* ---- coordinators: standalone transactional form ---------------------------------------- */
+sm_status sm_submit_route(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                          int divide_weights, const sm_route_buffers* b, char* err, size_t cap);
+sm_status sm_submit_grouping(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                             const sm_grouping_buffers* b, char* err, size_t cap);
+sm_status sm_submit_route_gather(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                                 const sm_route_gather_buffers* b, char* err, size_t cap);
+sm_status sm_submit_shared_ffn(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                               sm_format fmt, const sm_shared_buffers* b, char* err, size_t cap);
+sm_status sm_submit_gate_up(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                            sm_format fmt, const sm_gate_up_buffers* b, char* err, size_t cap);
+sm_status sm_submit_down(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                         sm_format fmt, const sm_down_buffers* b, char* err, size_t cap);
+sm_status sm_submit_swiglu(sm_context* ctx, void* stream, uint32_t rows, uint32_t width,
+                           const sm_swiglu_buffers* b, char* err, size_t cap);
+sm_status sm_submit_combine(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                            const sm_combine_buffers* b, char* err, size_t cap);
+sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                               const sm_layer_formats* formats, const sm_layer_buffers* b,
+                               char* err, size_t cap);
+
+/* ---- after completion ----------------------------------------------------------------- */
+/* Synchronises `stream`, then reads the plan's `bad` count and up to two status words
+ * (null views are skipped and read as 0). The reference's caller contract
+ * (prefill_moe_full_pipeline.hpp:44-46). */
+sm_status sm_read_layer_status(sm_context* ctx, void* stream, sm_view plan, sm_view gate_up_status,
+                               sm_view down_status, uint32_t* bad, uint32_t* gate_up_bits,
+                               uint32_t* down_bits);
+
+/* ---- synthetic inputs (host, deterministic; used by tests and the benchmark) ------------ */
+/* out[i] = N(0, sigma) from SplitMix64(seed, stream, i) + Box-Muller, as F32. */
+void sm_synth_normal_f32(uint64_t seed, uint64_t stream, float sigma, float* out, uint64_t n);
+/* Same values rounded to F16 (RNE) / BF16 (RNE). */
+void sm_synth_normal_f16(uint64_t seed, uint64_t stream, float sigma, uint16_t* out, uint64_t n);
+void sm_synth_normal_bf16(uint64_t seed, uint64_t stream, float sigma, uint16_t* out, uint64_t n);
+/* Quantizes rows*k F32 values (row-major [rows][k]) to `fmt` blocks. */
+sm_status sm_quantize(sm_format fmt, const float* in, uint64_t rows, uint64_t k, uint8_t* out);
+/* Generates N(0, sigma) weights for `rows` rows of `k` and quantizes them directly. */
+sm_status sm_synth_quantized(sm_format fmt, uint64_t seed, uint64_t stream, float sigma,
+                             uint64_t rows, uint64_t k, uint8_t* out);
+
+/* Library build identity. */
+uint32_t sm_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* STRATA_MOE_H */

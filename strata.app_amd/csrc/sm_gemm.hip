@@ -1,0 +1,299 @@
+// Grouped expert products and the dense shared-expert products for gfx950.
+//
+// Workgroup tile: 64 rows x 128 weight columns, 256 threads (4 wave64s). Wave w owns two
+// 16-column groups (c0, c1) and all 64 rows as four 16x16 MFMA accumulators per group.
+//   gate/up: c0 = gate rows j, c1 = up rows j for j in [64*nt + 16w, +16), so the SwiGLU
+//            epilogue pairs gate and up values that sit in the same lane and register;
+//   down:    c0, c1 = output columns [128*nt + 32w, +16) and [128*nt + 32w + 16, +16).
+// The K dimension runs in 256-value slabs. Each lane decodes its own weight values
+// straight into the MFMA B-operand layout (no LDS round trip for weights); the 64 x 256
+// activation slab is staged in LDS and shared by the four waves.
+// Routed workgroups walk the grouping's 64-entry tile list; the flat workgroup id is
+// remapped so that consecutive work items (the column tiles of one row tile) land on
+// the same XCD and share its L2.
+#include "sm_device.h"
+#include "sm_launch.h"
+
+namespace sm {
+namespace {
+
+constexpr int kRows = 64;
+constexpr int kSlab = 256;
+constexpr int kLdsRow = kSlab + 8;  // halves
+
+enum Mode { kGateUp = 0, kDown = 1 };
+
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t nb) {
+    // Hardware dispatches workgroup b to XCD b % 8; give each XCD a contiguous run of items.
+    const uint32_t per = nb >> 3;
+    return (b & 7u) * per + (b >> 3);
+}
+
+template <class Frag>
+__device__ __forceinline__ void tile_mma(const _Float16* __restrict__ a_rows, uint32_t a0,
+                                         uint32_t a_last, uint32_t K, const uint8_t* w0row,
+                                         const uint8_t* w1row, _Float16* sa, float4v (&acc0)[4],
+                                         float4v (&acc1)[4]) {
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    constexpr int kSB = SlabBytes<Frag>::value;
+    const uint32_t n_slabs = (K + kSlab - 1) / kSlab;
+    for (uint32_t sb = 0; sb < n_slabs; ++sb) {
+        const uint32_t k0 = sb * kSlab;
+        const bool kok = k0 + 64u * g < K;
+        Frag f0, f1;
+        if (kok) {
+            f0.load(w0row + uint64_t(sb) * kSB, g);
+            f1.load(w1row + uint64_t(sb) * kSB, g);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = tid + 256 * i;
+            const int r = c >> 5, cc = c & 31;
+            uint32_t row = a0 + r;
+            if (row > a_last) row = a_last;
+            const uint32_t kk = k0 + 8 * cc;
+            half8 v;
+            if (kk < K) v = *reinterpret_cast<const half8*>(a_rows + uint64_t(row) * K + kk);
+            else v = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            *reinterpret_cast<half8*>(sa + r * kLdsRow + 8 * cc) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const half8 zero{0, 0, 0, 0, 0, 0, 0, 0};
+            const half8 b0 = kok ? f0.step(s) : zero;
+            const half8 b1 = kok ? f1.step(s) : zero;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const half8 a = *reinterpret_cast<const half8*>(sa + (16 * rb + n) * kLdsRow + 64 * g + 8 * s);
+                acc0[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b0, acc0[rb], 0, 0, 0);
+                acc1[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc1[rb], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Zero the block's output tile for rows [r0, r1) (route order for gate/up, entry order for
+// the down tile, as the reference's zero paths do: prefill_moe.metal:556-601).
+template <int MODE>
+__device__ void zero_tile(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_t nt) {
+    if (MODE == kGateUp) {
+        for (uint32_t i = threadIdx.x; i < 64u * 64u; i += 256u) {
+            const uint32_t r = r0 + i / 64u, c = nt * 64u + i % 64u;
+            if (r < r1 && r < g.n_entries) g.out_h[uint64_t(r) * g.n_out + c] = _Float16(0.0f);
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < 64u * 128u; i += 256u) {
+            const uint32_t r = r0 + i / 128u, c = nt * 128u + i % 128u;
+            if (r < r1 && r < g.n_entries) g.out_f[uint64_t(r) * g.n_out + c] = 0.0f;
+        }
+    }
+}
+
+template <class Frag, int MODE>
+__global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t n_ntiles, uint32_t total) {
+    __shared__ __attribute__((aligned(16))) _Float16 sa[kRows * kLdsRow];
+    __shared__ uint32_t s_flag;
+    const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+    if (w >= total) return;
+    const uint32_t tile_index = w / n_ntiles, nt = w % n_ntiles;
+    const Plan* p = g.plan;
+    const uint32_t N = g.n_entries;
+    if (threadIdx.x == 0) s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_flag & 2u) {  // invalid plan or permutation: every tile slot writes zeros
+        zero_tile<MODE>(g, tile_index * 64u, tile_index * 64u + 64u, nt);
+        return;
+    }
+    if (tile_index >= p->n_tiles) return;
+    const uint32_t tg = g.tiles[2 * tile_index], a0 = g.tiles[2 * tile_index + 1];
+    bool ok = tg < p->n_groups;
+    uint32_t gfirst = 0, gend = 0;
+    int32_t ex = -1;
+    if (ok) {
+        const int32_t f = p->grp_start[tg], e = p->grp_start[tg + 1];
+        ex = p->grp_e[tg];
+        ok = f >= 0 && e > f && uint32_t(e) <= p->n_entries && ex >= 0 && uint32_t(ex) < g.n_experts;
+        if (ok) {
+            gfirst = uint32_t(f);
+            gend = uint32_t(e);
+            ok = a0 >= gfirst && a0 < gend && (a0 - gfirst) % 64u == 0u;
+        }
+    }
+    if (!ok) {
+        if (threadIdx.x == 0) atomicOr(g.status, 2u);
+        zero_tile<MODE>(g, tile_index * 64u, tile_index * 64u + 64u, nt);
+        return;
+    }
+    const uint32_t a1 = a0 + 64u < gend ? a0 + 64u : gend;
+    const uint64_t* addr = g.addresses + 3u * uint32_t(ex);
+    const uint8_t* w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
+    const uint8_t* w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
+    if (w0 == nullptr || w1 == nullptr) {
+        if (threadIdx.x == 0) atomicOr(g.status, 1u);
+        if (MODE == kGateUp) {
+            zero_tile<MODE>(g, a0, a1, nt);
+        } else {  // down rows live in route order
+            for (uint32_t i = threadIdx.x; i < 64u * 128u; i += 256u) {
+                const uint32_t a = a0 + i / 128u, c = nt * 128u + i % 128u;
+                if (a >= a1) continue;
+                const uint32_t d = uint32_t(g.dst[a]);
+                if (d < N) g.out_f[uint64_t(d) * g.n_out + c] = 0.0f;
+                else atomicOr(g.status, 2u);
+            }
+        }
+        return;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, gq = lane >> 4;
+    uint32_t col0, col1;
+    if (MODE == kGateUp) { col0 = nt * 64u + 16u * wave + n; col1 = col0; }
+    else { col0 = nt * 128u + 32u * wave + n; col1 = col0 + 16u; }
+    float4v acc0[4], acc1[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
+    tile_mma<Frag>(g.a, a0, a1 - 1u, g.k, w0 + uint64_t(col0) * g.row_bytes, w1 + uint64_t(col1) * g.row_bytes,
+                   sa, acc0, acc1);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = a0 + 16u * rb + 4u * gq + i;
+            if (a >= a1) continue;
+            if (MODE == kGateUp) {
+                g.out_h[uint64_t(a) * g.n_out + col0] = half_sat(silu(acc0[rb][i]) * acc1[rb][i]);
+            } else {
+                const uint32_t d = uint32_t(g.dst[a]);
+                if (d < N) {
+                    g.out_f[uint64_t(d) * g.n_out + col0] = acc0[rb][i];
+                    g.out_f[uint64_t(d) * g.n_out + col1] = acc1[rb][i];
+                } else {
+                    atomicOr(g.status, 2u);
+                    g.out_f[uint64_t(a) * g.n_out + col0] = 0.0f;
+                    g.out_f[uint64_t(a) * g.n_out + col1] = 0.0f;
+                }
+            }
+        }
+}
+
+// Dense (shared-expert) products: rows are tokens in 64-row tiles.
+template <class Frag, int MODE>
+__global__ __launch_bounds__(256) void dense_gemm_kernel(DenseGemm g, uint32_t n_ntiles, uint32_t total) {
+    __shared__ __attribute__((aligned(16))) _Float16 sa[kRows * kLdsRow];
+    const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+    if (w >= total) return;
+    const uint32_t mt = w / n_ntiles, nt = w % n_ntiles;
+    const uint32_t r0 = mt * 64u;
+    const uint32_t r1 = r0 + 64u < g.rows ? r0 + 64u : g.rows;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, gq = lane >> 4;
+    uint32_t col0, col1;
+    const uint8_t *w0, *w1;
+    if (MODE == kGateUp) {
+        col0 = nt * 64u + 16u * wave + n; col1 = col0; w0 = g.w0; w1 = g.w1;
+    } else {
+        col0 = nt * 128u + 32u * wave + n; col1 = col0 + 16u; w0 = g.w0; w1 = g.w0;
+    }
+    float4v acc0[4], acc1[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
+    tile_mma<Frag>(g.a, r0, r1 - 1u, g.k, w0 + uint64_t(col0) * g.row_bytes, w1 + uint64_t(col1) * g.row_bytes,
+                   sa, acc0, acc1);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = r0 + 16u * rb + 4u * gq + i;
+            if (r >= r1) continue;
+            if (MODE == kGateUp) {
+                g.out_h[uint64_t(r) * g.n_out + col0] = half_sat(silu(acc0[rb][i]) * acc1[rb][i]);
+            } else {
+                g.out_f[uint64_t(r) * g.n_out + col0] = acc0[rb][i];
+                g.out_f[uint64_t(r) * g.n_out + col1] = acc1[rb][i];
+            }
+        }
+}
+
+// gl[t] = sum_k x[t,k] * gv[k]: one wave per token, lane-strided F32 partial sums reduced
+// by a fixed xor butterfly.
+template <bool BF16>
+__global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restrict__ x,
+                                                         const uint16_t* __restrict__ gv,
+                                                         float* __restrict__ gl, uint32_t rows, uint32_t d) {
+    const uint32_t t = (blockIdx.x * 256u + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    if (t >= rows) return;
+    float s = 0.0f;
+    for (uint32_t k = lane; k < d; k += 64u) {
+        const uint16_t b = gv[k];
+        const float wv = BF16 ? __builtin_bit_cast(float, uint32_t(b) << 16) : float(bits_f16(b));
+        s = __builtin_fmaf(float(x[uint64_t(t) * d + k]), wv, s);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s = s + __shfl_xor(s, off);
+    if (lane == 0) gl[t] = s;
+}
+
+template <class Frag, int MODE>
+hipError_t launch_routed(const RoutedGemm& g, hipStream_t s) {
+    const uint32_t n_ntiles = MODE == kGateUp ? g.n_out / 64u : g.n_out / 128u;
+    const uint32_t total = g.tile_capacity * n_ntiles;
+    const uint32_t blocks = (total + 7u) & ~7u;
+    routed_gemm_kernel<Frag, MODE><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
+    return hipGetLastError();
+}
+
+template <class Frag, int MODE>
+hipError_t launch_dense(const DenseGemm& g, hipStream_t s) {
+    const uint32_t n_ntiles = MODE == kGateUp ? g.n_out / 64u : g.n_out / 128u;
+    const uint32_t total = ((g.rows + 63u) / 64u) * n_ntiles;
+    const uint32_t blocks = (total + 7u) & ~7u;
+    dense_gemm_kernel<Frag, MODE><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gate_up(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
+    switch (fmt) {
+        case Fmt::Q8_0: return launch_routed<FragQ80, kGateUp>(g, s);
+        case Fmt::Q4_K: return launch_routed<FragQ4K, kGateUp>(g, s);
+        case Fmt::Q2_K: return launch_routed<FragQ2K, kGateUp>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
+    switch (fmt) {
+        case Fmt::Q8_0: return launch_routed<FragQ80, kDown>(g, s);
+        case Fmt::Q4_K: return launch_routed<FragQ4K, kDown>(g, s);
+        case Fmt::Q2_K: return launch_routed<FragQ2K, kDown>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dense_gate_up(Fmt fmt, const DenseGemm& g, hipStream_t s) {
+    switch (fmt) {
+        case Fmt::F16: return launch_dense<FragF16, kGateUp>(g, s);
+        case Fmt::BF16: return launch_dense<FragBF16, kGateUp>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dense_down(Fmt fmt, const DenseGemm& g, hipStream_t s) {
+    switch (fmt) {
+        case Fmt::F16: return launch_dense<FragF16, kDown>(g, s);
+        case Fmt::BF16: return launch_dense<FragBF16, kDown>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gate_logit(Fmt fmt, const _Float16* x, const uint8_t* gv, float* gl, uint32_t rows,
+                             uint32_t d, hipStream_t s) {
+    const uint32_t blocks = (rows + 3u) / 4u;
+    const uint16_t* v = reinterpret_cast<const uint16_t*>(gv);
+    if (fmt == Fmt::BF16) gate_logit_kernel<true><<<blocks, 256, 0, s>>>(x, v, gl, rows, d);
+    else gate_logit_kernel<false><<<blocks, 256, 0, s>>>(x, v, gl, rows, d);
+    return hipGetLastError();
+}
+
+}  // namespace sm

@@ -1,0 +1,89 @@
+// Internal launch interface between the host coordinators (sm_runtime.cpp) and the gfx950
+// kernels. Plain pointers and sizes only; every launcher assumes its arguments were
+// validated by the coordinator (shapes, extents, alignment) and checks nothing itself.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sm {
+
+// PfPlan (the reference's prefill_moe.metal:23-33): 6180 bytes inside a 6400-byte slot.
+struct Plan {
+    uint32_t n_groups, n_entries, n_miss, skip, n_tiles, bad, pad[2];
+    int32_t grp_e[512];
+    int32_t grp_res[512];
+    int32_t grp_start[513];
+};
+static_assert(sizeof(Plan) == 6180, "PfPlan layout");
+
+constexpr uint32_t kCountTile = 256;   // histogram tile (entries)
+constexpr uint32_t kExpertTile = 64;   // tile-list tile (entries)
+constexpr uint32_t kPlanSlotBytes = 6400;
+
+enum class Fmt : int { Q8_0 = 1, Q4_K = 2, Q2_K = 3, F16 = 4, BF16 = 5 };
+
+// ---- route ----
+// bias (F32 [E]) may be null.
+hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bias, float* logits,
+                              uint32_t rows, uint32_t d, uint32_t n_experts, hipStream_t s);
+hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, uint32_t rows,
+                             uint32_t n_experts, uint32_t top_k, int divide, hipStream_t s);
+
+// ---- grouping ----
+// hist has ceil(N/256) + 1 rows of n_experts u32; the extra last row holds each expert's
+// first grouped slot.
+hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                           uint32_t* hist, Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst,
+                           hipStream_t s);
+hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
+                         const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
+
+// ---- expert stage validation (the reference's plan/destination validators) ----
+hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status,
+                                uint32_t n_entries, uint32_t n_experts, uint32_t tile_capacity,
+                                hipStream_t s);
+hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bitset, uint32_t* status,
+                                       uint32_t n_entries, hipStream_t s);
+
+// ---- grouped expert products ----
+struct RoutedGemm {
+    const uint64_t* addresses;  // device [E][3] (gate, up, down)
+    const _Float16* a;          // grouped rows [N][K]
+    const Plan* plan;
+    const uint32_t* tiles;      // {group, first_entry} pairs
+    const int32_t* dst;         // down only
+    _Float16* out_h;            // gate/up: [N][I]
+    float* out_f;               // down: [N][d] route order
+    uint32_t* status;
+    uint32_t n_entries, n_experts, tile_capacity;
+    uint32_t k;                 // reduction length (d for gate/up, I for down)
+    uint32_t n_out;             // output columns (I for gate/up, d for down)
+    uint64_t row_bytes;         // bytes of one weight row of k values
+};
+hipError_t launch_gate_up(Fmt fmt, const RoutedGemm& g, hipStream_t s);
+hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s);
+
+struct DenseGemm {
+    const _Float16* a;          // [rows][k]
+    const uint8_t* w0;          // gate/up: gate [n][k]; down: W [n_out][k]
+    const uint8_t* w1;          // gate/up: up   [n][k]
+    _Float16* out_h;            // gate/up output [rows][n]
+    float* out_f;               // down output [rows][n_out]
+    uint32_t rows, k, n_out;
+    uint64_t row_bytes;
+};
+hipError_t launch_dense_gate_up(Fmt fmt, const DenseGemm& g, hipStream_t s);
+hipError_t launch_dense_down(Fmt fmt, const DenseGemm& g, hipStream_t s);
+// gl[t] = sum_k x[t,k] * gv[k] (F16 or BF16 gate vector), F32 accumulation.
+hipError_t launch_gate_logit(Fmt fmt, const _Float16* x, const uint8_t* gv, float* gl, uint32_t rows,
+                             uint32_t d, hipStream_t s);
+
+// ---- post ops ----
+hipError_t launch_swiglu(const float* gate, const float* up, _Float16* out, uint64_t n,
+                         hipStream_t s);
+hipError_t launch_combine(const float* parts, const float* weights, const float* shared,
+                          const float* gl, float* out, uint32_t rows, uint32_t top_k, uint32_t d,
+                          hipStream_t s);
+
+}  // namespace sm

@@ -1,0 +1,485 @@
+// Router GEMM, softmax top-k, stable expert grouping, F16 row gather, and the plan /
+// destination validators for gfx950.
+#include "sm_device.h"
+#include "sm_launch.h"
+
+namespace sm {
+namespace {
+
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kWeightFloor = 6.103515625e-5f;  // 2^-14
+
+// ---------------------------------------------------------------------------------------
+// Router GEMM: logits[t,e] = sum_k x[t,k] * W[e,k], F16 activations, F32 weights.
+// Each F32 weight is split into an F16 head and an F16 tail scaled by 2^11
+// (w = hi + lo * 2^-11 to ~2^-24 relative); two MFMA accumulators carry the head and tail
+// products and are merged as fma(lo, 2^-11, hi). Tile: 64 tokens x 64 experts per
+// 256-thread workgroup; wave w owns experts 16w..16w+15 of the tile.
+// ---------------------------------------------------------------------------------------
+constexpr int kRouterRows = 64;
+constexpr int kRouterCols = 64;
+constexpr int kSlab = 256;
+constexpr int kLdsRow = kSlab + 8;  // halves; padding breaks row-to-bank aliasing
+
+__global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ bias,
+                                                          float* __restrict__ logits,
+                                                          uint32_t rows, uint32_t d, uint32_t E) {
+    __shared__ __attribute__((aligned(16))) _Float16 sa[kRouterRows * kLdsRow];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const uint32_t t0 = blockIdx.x * kRouterRows;
+    const uint32_t e0 = blockIdx.y * kRouterCols;
+    const uint32_t e = e0 + 16 * wave + n;
+    const bool e_ok = e < E;
+    const float* wrow = w + uint64_t(e_ok ? e : 0) * d;
+    float4v acc_hi[4], acc_lo[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
+    for (uint32_t k0 = 0; k0 < d; k0 += kSlab) {
+        // Stage 64 token rows x 256 values of x (16 B per thread per step).
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = tid + 256 * i;
+            const int r = c >> 5, cc = c & 31;
+            uint32_t t = t0 + r;
+            if (t >= rows) t = rows - 1;
+            const half8 v = *reinterpret_cast<const half8*>(x + uint64_t(t) * d + k0 + 8 * cc);
+            *reinterpret_cast<half8*>(sa + r * kLdsRow + 8 * cc) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            half8 bh, bl;
+            const int kk = 64 * g + 8 * s;
+            if (e_ok) {
+                const float4v w0 = *reinterpret_cast<const float4v*>(wrow + k0 + kk);
+                const float4v w1 = *reinterpret_cast<const float4v*>(wrow + k0 + kk + 4);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float wf = i < 4 ? w0[i] : w1[i - 4];
+                    const _Float16 h = _Float16(wf);
+                    bh[i] = h;
+                    bl[i] = _Float16((wf - float(h)) * 2048.0f);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) { bh[i] = 0; bl[i] = 0; }
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const half8 a = *reinterpret_cast<const half8*>(sa + (16 * rb + n) * kLdsRow + kk);
+                acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_hi[rb], 0, 0, 0);
+                acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_lo[rb], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    if (!e_ok) return;
+    const float b = bias != nullptr ? bias[e] : 0.0f;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t t = t0 + 16 * rb + 4 * g + i;
+            if (t < rows) logits[uint64_t(t) * E + e] = __builtin_fmaf(acc_lo[rb][i], 4.8828125e-4f, acc_hi[rb][i]) + b;
+        }
+}
+
+// ---------------------------------------------------------------------------------------
+// Softmax top-k. One token per half-wave: the 32 lanes of a half replay the reference's
+// 32-lane SIMD group exactly (moe.metal:28-86) — lane L holds experts L + 32i, the max and
+// sum butterflies use xor offsets 16..1, and each round's argmax butterfly prefers the
+// larger value and, on equal values, the lower expert id. Slots past E are padding: they
+// take no part in the sums and hold -inf so they are never selected (top_k <= E).
+// ---------------------------------------------------------------------------------------
+template <int NV>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
+                                                         int32_t* __restrict__ ids,
+                                                         float* __restrict__ weights,
+                                                         uint32_t rows, uint32_t E, uint32_t K,
+                                                         int divide) {
+    const uint32_t L = threadIdx.x & 31u;
+    const uint32_t t = (blockIdx.x * 256u + threadIdx.x) >> 5;
+    const bool live = t < rows;
+    const float* row = logits + uint64_t(live ? t : 0u) * E;
+    float v[NV];
+    float mx = kNegInf;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t idx = L + 32u * i;
+        v[i] = (live && idx < E) ? row[idx] : kNegInf;
+        mx = __builtin_fmaxf(mx, v[i]);
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (L + 32u * i < E) {
+            v[i] = exp_cw(v[i] - mx);
+            sum = sum + v[i];
+        }
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off);
+    const float recip = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (L + 32u * i < E) {
+            v[i] = v[i] * recip;
+            if (__builtin_isnan(v[i])) v[i] = -3.40282346638528859812e+38f;
+        } else {
+            v[i] = kNegInf;
+        }
+    }
+    float selected = 0.0f, sel_sum = 0.0f;
+    for (uint32_t rank = 0; rank < K; ++rank) {
+        float best = v[0];
+        int32_t who = int32_t(L);
+#pragma unroll
+        for (int i = 1; i < NV; ++i)
+            if (v[i] > best) { best = v[i]; who = int32_t(L + 32u * i); }
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) {
+            const float ob = __shfl_xor(best, off);
+            const int32_t ow = __shfl_xor(who, off);
+            if (ob > best || (ob == best && ow < who)) { best = ob; who = ow; }
+        }
+        if ((uint32_t(who) & 31u) == L) {
+            const int slot = who >> 5;
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+                if (i == slot) v[i] = kNegInf;
+            if (live) ids[uint64_t(t) * K + rank] = who;
+            sel_sum = sel_sum + best;
+        }
+        if (rank == L) selected = best;
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) sel_sum = sel_sum + __shfl_xor(sel_sum, off);
+    const float ssum = __builtin_fmaxf(sel_sum, kWeightFloor);
+    const float inv = 1.0f / ssum;
+    if (live && L < K) weights[uint64_t(t) * K + L] = divide ? selected / ssum : selected * inv;
+}
+
+// ---------------------------------------------------------------------------------------
+// Grouping. Results equal a stable counting sort of the valid entries by expert id:
+//   count   one 256-entry tile per workgroup, LDS histogram, raw counts to hist[tile][e]
+//   colscan per expert column, exclusive prefix over tiles (32 tile slices per column in
+//           parallel); column totals to the extra row hist[n_tiles][e]
+//   plan    one workgroup: block scans over experts give each expert's first slot, group
+//           index and first tile; writes the PfPlan slot and the 64-entry tile list, and
+//           replaces hist[n_tiles][e] by the expert's first slot
+//   scatter one 256-entry tile per workgroup: hist row += first slot (the reference's
+//           "cursor at tile start"); stable in-tile rank from per-wave ballot matching of
+//           the 9-bit ids plus the counts of earlier waves; src[slot] = i/k, dst[slot] = i
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void group_count_kernel(const int32_t* __restrict__ ids, uint32_t N,
+                                                          uint32_t E, uint32_t* __restrict__ hist) {
+    __shared__ uint32_t cnt[512];
+    const uint32_t tile = blockIdx.x, tid = threadIdx.x;
+    for (uint32_t e = tid; e < E; e += 256) cnt[e] = 0;
+    __syncthreads();
+    const uint64_t entry = uint64_t(tile) * kCountTile + tid;
+    if (entry < N) {
+        const int32_t id = ids[entry];
+        if (id >= 0 && uint32_t(id) < E) atomicAdd(&cnt[id], 1u);
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += 256) hist[uint64_t(tile) * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(1024) void group_colscan_kernel(uint32_t* __restrict__ hist, uint32_t E,
+                                                             uint32_t n_tiles) {
+    __shared__ uint32_t part[32][33];
+    const uint32_t el = threadIdx.x & 31u, slice = threadIdx.x >> 5;
+    const uint32_t e = blockIdx.x * 32u + el;
+    const uint32_t per = (n_tiles + 31u) / 32u;
+    const uint32_t t_begin = slice * per;
+    const uint32_t t_end = t_begin + per < n_tiles ? t_begin + per : n_tiles;
+    uint32_t local = 0;
+    if (e < E)
+        for (uint32_t t = t_begin; t < t_end; ++t) local += hist[uint64_t(t) * E + e];
+    part[slice][el] = local;
+    __syncthreads();
+    uint32_t run = 0;
+    for (uint32_t s = 0; s < slice; ++s) run += part[s][el];
+    if (e >= E) return;
+    if (slice == 31u) hist[uint64_t(n_tiles) * E + e] = run + local;
+    for (uint32_t t = t_begin; t < t_end; ++t) {
+        const uint64_t h = uint64_t(t) * E + e;
+        const uint32_t c = hist[h];
+        hist[h] = run;
+        run += c;
+    }
+}
+
+// Exclusive scan over the 512 threads of a workgroup; returns the prefix and the total.
+__device__ __forceinline__ uint32_t block_scan_512(uint32_t v, uint32_t* wave_tot, uint32_t& total) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(inc, off);
+        if (lane >= uint32_t(off)) inc += o;
+    }
+    if (lane == 63u) wave_tot[wave] = inc;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t w = 0; w < 8; ++w) {
+        if (w < wave) before += wave_tot[w];
+        all += wave_tot[w];
+    }
+    __syncthreads();
+    total = all;
+    return before + inc - v;
+}
+
+__global__ __launch_bounds__(512) void group_plan_kernel(uint32_t* __restrict__ hist, uint32_t E, uint32_t N,
+                                                         uint32_t n_tiles, Plan* __restrict__ plan,
+                                                         uint32_t* __restrict__ tiles) {
+    __shared__ uint32_t wave_tot[8];
+    const uint32_t e = threadIdx.x;
+    const uint32_t count = e < E ? hist[uint64_t(n_tiles) * E + e] : 0u;
+    uint32_t total_count, total_groups, total_tiles;
+    const uint32_t first = block_scan_512(count, wave_tot, total_count);
+    const uint32_t grp = block_scan_512(count ? 1u : 0u, wave_tot, total_groups);
+    const uint32_t ntile_e = (count + kExpertTile - 1) / kExpertTile;
+    const uint32_t tstart = block_scan_512(ntile_e, wave_tot, total_tiles);
+    // Whole 6400-byte slot: every word defined (unused group slots -1 / 0, tail zero).
+    uint32_t* words = reinterpret_cast<uint32_t*>(plan);
+    for (uint32_t i = e; i < kPlanSlotBytes / 4; i += 512) {
+        uint32_t val = 0;
+        if (i >= 8 && i < 8 + 1024) val = 0xffffffffu;  // grp_e[], grp_res[] = -1
+        words[i] = val;
+    }
+    __syncthreads();
+    if (count) {
+        plan->grp_e[grp] = int32_t(e);
+        plan->grp_res[grp] = 1;
+        plan->grp_start[grp] = int32_t(first);
+        for (uint32_t j = 0; j < ntile_e; ++j) {
+            tiles[2 * (tstart + j)] = grp;
+            tiles[2 * (tstart + j) + 1] = first + kExpertTile * j;
+        }
+    }
+    if (e < E) hist[uint64_t(n_tiles) * E + e] = first;
+    if (e == 0) {
+        plan->n_groups = total_groups;
+        plan->n_entries = N;
+        plan->n_miss = 0;
+        plan->skip = 1;
+        plan->n_tiles = total_tiles;
+        plan->bad = N - total_count;
+        plan->grp_start[total_groups] = int32_t(total_count);
+    }
+}
+
+__global__ __launch_bounds__(256) void group_scatter_kernel(const int32_t* __restrict__ ids, uint32_t N,
+                                                            uint32_t K, uint32_t E, uint32_t n_tiles,
+                                                            uint32_t* __restrict__ hist,
+                                                            int32_t* __restrict__ src,
+                                                            int32_t* __restrict__ dst) {
+    __shared__ uint32_t wcnt[4][512];
+    __shared__ uint32_t base[512];
+    const uint32_t tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    for (uint32_t i = tid; i < 4 * 512; i += 256) (&wcnt[0][0])[i] = 0;
+    for (uint32_t e = tid; e < E; e += 256) {
+        const uint64_t h = uint64_t(tile) * E + e;
+        const uint32_t fin = hist[h] + hist[uint64_t(n_tiles) * E + e];
+        hist[h] = fin;
+        base[e] = fin;
+    }
+    const uint64_t entry = uint64_t(tile) * kCountTile + tid;
+    const int32_t id = entry < N ? ids[entry] : -1;
+    const bool valid = id >= 0 && uint32_t(id) < E;
+    const uint32_t key = valid ? uint32_t(id) : 1023u;
+    uint64_t match = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+        const bool bit = (key >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        match &= bit ? bal : ~bal;
+    }
+    const uint64_t lt = (1ull << lane) - 1ull;
+    const uint32_t rank = __popcll(match & lt);
+    const uint64_t gt = lane == 63u ? 0ull : (~0ull << (lane + 1u));
+    __syncthreads();
+    if (valid && (match & gt) == 0ull) wcnt[wave][id] = rank + 1u;
+    __syncthreads();
+    if (!valid) return;
+    uint32_t slot = base[id] + rank;
+    for (uint32_t w = 0; w < wave; ++w) slot += wcnt[w][id];
+    src[slot] = int32_t(entry / K);
+    dst[slot] = int32_t(entry);
+}
+
+// Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count; 16 bytes per thread,
+// 4 independent copies in flight per thread. The plan header is checked first as in the
+// reference's gather (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
+__global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t rows,
+                                                     uint32_t vpr, const int32_t* __restrict__ src,
+                                                     const Plan* __restrict__ plan, uint32_t N,
+                                                     u32x4* __restrict__ xs) {
+    const uint32_t ng = plan->n_groups;
+    if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) return;
+    const int32_t sorted_signed = plan->grp_start[ng];
+    if (sorted_signed < 0 || uint32_t(sorted_signed) != N - plan->bad) return;
+    const uint64_t total = uint64_t(uint32_t(sorted_signed)) * vpr;
+    const uint64_t base = uint64_t(blockIdx.x) * 1024u + threadIdx.x;
+    u32x4 v[4];
+    uint64_t out[4];
+    bool ok[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint64_t idx = base + 256u * j;
+        ok[j] = idx < total;
+        out[j] = idx;
+        if (ok[j]) {
+            const uint64_t a = idx / vpr, c = idx % vpr;
+            const int32_t s = src[a];
+            ok[j] = s >= 0 && uint32_t(s) < rows;
+            if (ok[j]) v[j] = x[uint64_t(s) * vpr + c];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (ok[j]) xs[out[j]] = v[j];
+}
+
+// ---------------------------------------------------------------------------------------
+// Expert-stage validation (prefill_moe.metal:603-733): status is cleared, then bit 1 set
+// when the plan header, the tile chain, or the destination permutation is inconsistent.
+// ---------------------------------------------------------------------------------------
+__device__ bool plan_header_valid(const Plan* p, uint32_t N, uint32_t E, uint32_t cap) {
+    if (p->bad != 0u || p->n_groups == 0u || p->n_groups > E || p->n_groups > 512u ||
+        p->n_entries != N || p->n_tiles > cap || p->n_tiles > p->n_entries ||
+        p->grp_start[0] != 0 || p->grp_start[p->n_groups] != int32_t(N))
+        return false;
+    uint32_t expected = 0;
+    int32_t prev_end = 0;
+    for (uint32_t g = 0; g < p->n_groups; ++g) {
+        const int32_t first = p->grp_start[g], end = p->grp_start[g + 1], ex = p->grp_e[g];
+        if (first != prev_end || end <= first || uint32_t(end) > N || ex < 0 || uint32_t(ex) >= E)
+            return false;
+        if (g != 0u && ex <= p->grp_e[g - 1]) return false;
+        prev_end = end;
+        const uint32_t c = uint32_t(end - first);
+        expected += (c + kExpertTile - 1) / kExpertTile;
+        if (expected > cap) return false;
+    }
+    return prev_end == int32_t(N) && expected == p->n_tiles;
+}
+
+__global__ __launch_bounds__(256) void plan_validate_kernel(const Plan* __restrict__ p,
+                                                            const uint32_t* __restrict__ tiles,
+                                                            uint32_t* __restrict__ status, uint32_t N,
+                                                            uint32_t E, uint32_t cap) {
+    __shared__ uint32_t header_ok;
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) {
+        *status = 0u;
+        header_ok = plan_header_valid(p, N, E, cap) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!header_ok) {
+        if (tid == 0) atomicOr(status, 2u);
+        return;
+    }
+    for (uint32_t i = tid; i < p->n_tiles; i += 256) {
+        const uint32_t tg = tiles[2 * i], ty = tiles[2 * i + 1];
+        bool ok = tg < p->n_groups;
+        if (ok) {
+            const uint32_t first = uint32_t(p->grp_start[tg]), end = uint32_t(p->grp_start[tg + 1]);
+            ok = ty >= first && ty < end && (ty - first) % kExpertTile == 0u;
+            if (i == 0u) {
+                ok = ok && tg == 0u && ty == 0u;
+            } else {
+                const uint32_t pg = tiles[2 * (i - 1)], py = tiles[2 * (i - 1) + 1];
+                if (pg >= p->n_groups) ok = false;
+                else if (pg == tg) ok = ok && ty == py + kExpertTile;
+                else if (pg + 1u == tg) ok = ok && py + kExpertTile >= uint32_t(p->grp_start[pg + 1]) && ty == first;
+                else ok = false;
+            }
+            if (i + 1u == p->n_tiles) ok = ok && tg + 1u == p->n_groups && ty + kExpertTile >= end;
+        }
+        if (!ok) atomicOr(status, 2u);
+    }
+}
+
+__global__ __launch_bounds__(256) void bitset_clear_kernel(uint32_t* __restrict__ bits, uint32_t words) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < words) bits[i] = 0u;
+}
+
+__global__ __launch_bounds__(256) void destination_validate_kernel(const int32_t* __restrict__ dst,
+                                                                   uint32_t* __restrict__ bits,
+                                                                   uint32_t* __restrict__ status,
+                                                                   uint32_t N) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t d = uint32_t(dst[i]);
+    if (d >= N) { atomicOr(status, 2u); return; }
+    const uint32_t mask = 1u << (d % 32u);
+    if (atomicOr(&bits[d / 32u], mask) & mask) atomicOr(status, 2u);
+}
+
+}  // namespace
+
+hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bias, float* logits,
+                              uint32_t rows, uint32_t d, uint32_t E, hipStream_t s) {
+    const dim3 grid((rows + kRouterRows - 1) / kRouterRows, (E + kRouterCols - 1) / kRouterCols);
+    router_gemm_kernel<<<grid, 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, uint32_t rows,
+                             uint32_t E, uint32_t K, int divide, hipStream_t s) {
+    const uint32_t blocks = (rows + 7u) / 8u;
+    const uint32_t nv = (E + 31u) / 32u;
+    if (nv <= 1) route_topk_kernel<1><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
+    else if (nv <= 2) route_topk_kernel<2><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
+    else if (nv <= 4) route_topk_kernel<4><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
+    else if (nv <= 8) route_topk_kernel<8><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
+    else route_topk_kernel<16><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
+    return hipGetLastError();
+}
+
+hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32_t E, uint32_t* hist,
+                           Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst, hipStream_t s) {
+    const uint32_t N = rows * K;
+    const uint32_t n_tiles = (N + kCountTile - 1) / kCountTile;
+    group_count_kernel<<<n_tiles, 256, 0, s>>>(ids, N, E, hist);
+    group_colscan_kernel<<<(E + 31) / 32, 1024, 0, s>>>(hist, E, n_tiles);
+    group_plan_kernel<<<1, 512, 0, s>>>(hist, E, N, n_tiles, plan, tiles);
+    group_scatter_kernel<<<n_tiles, 256, 0, s>>>(ids, N, K, E, n_tiles, hist, src, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
+                         const Plan* plan, uint32_t N, _Float16* xs, hipStream_t s) {
+    const uint32_t vpr = d / 8;
+    const uint64_t total = uint64_t(N) * vpr;
+    const uint32_t blocks = uint32_t((total + 1023) / 1024);
+    gather_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
+                                         reinterpret_cast<u32x4*>(xs));
+    return hipGetLastError();
+}
+
+hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status, uint32_t N,
+                                uint32_t E, uint32_t cap, hipStream_t s) {
+    plan_validate_kernel<<<1, 256, 0, s>>>(plan, tiles, status, N, E, cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bits, uint32_t* status, uint32_t N,
+                                       hipStream_t s) {
+    const uint32_t words = (N + 31) / 32;
+    bitset_clear_kernel<<<(words + 255) / 256, 256, 0, s>>>(bits, words);
+    destination_validate_kernel<<<(N + 255) / 256, 256, 0, s>>>(dst, bits, status, N);
+    return hipGetLastError();
+}
+
+}  // namespace sm

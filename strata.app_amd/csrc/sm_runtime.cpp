@@ -1,0 +1,876 @@
+// Host runtime and coordinators behind the C ABI in include/strata_moe.h.
+//
+// A segment is an ordered list of validated launches. Every coordinator first validates
+// all of its views (ownership, extent, alignment, aliasing) and only then appends its
+// launches; a failure poisons the segment so that commit refuses it and nothing reaches
+// the GPU — the reference's transactional encoder (encoder.mm:165-231,
+// context.mm:623-680), built on deferred launches because a HIP launch cannot be revoked.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/strata_moe.h"
+#include "sm_launch.h"
+
+struct sm_context {
+    int device = 0;
+    bool has_device = false;
+    std::mutex mu;
+    struct Alloc { uintptr_t ptr; uint64_t bytes; };
+    std::map<uint64_t, Alloc> buffers;
+    uint64_t next_handle = 1;
+};
+
+struct sm_segment {
+    sm_context* ctx = nullptr;
+    struct Step { std::string label; std::function<hipError_t(hipStream_t)> run; };
+    std::vector<Step> steps;
+    bool failed = false;
+    std::string error;
+};
+
+namespace {
+
+using sm::Fmt;
+
+// ---- small helpers --------------------------------------------------------------------
+
+bool mul_ok(std::initializer_list<uint64_t> f, uint64_t& out) {
+    out = 1;
+    for (uint64_t v : f) {
+        if (v != 0 && out > std::numeric_limits<uint64_t>::max() / v) return false;
+        out *= v;
+    }
+    return true;
+}
+
+uint64_t ceil_div(uint64_t a, uint64_t b) { return a / b + (a % b != 0 ? 1 : 0); }
+
+uint64_t fmt_row_bytes(int fmt, uint64_t k) {
+    switch (fmt) {
+        case SM_FMT_Q8_0: return k % 32 ? 0 : k / 32 * 34;
+        case SM_FMT_Q4_K: return k % 256 ? 0 : k / 256 * 144;
+        case SM_FMT_Q2_K: return k % 256 ? 0 : k / 256 * 84;
+        case SM_FMT_F16:
+        case SM_FMT_BF16: return 2 * k;
+    }
+    return 0;
+}
+
+bool routed_fmt(int f) { return f == SM_FMT_Q8_0 || f == SM_FMT_Q4_K || f == SM_FMT_Q2_K; }
+bool dense_fmt(int f) { return f == SM_FMT_F16 || f == SM_FMT_BF16; }
+
+// K granularity of the expert kernels: whole 256-value slabs for the K-quants and dense
+// rows; 64-value lane groups for Q8_0.
+bool k_ok(int fmt, uint64_t k) {
+    if (fmt == SM_FMT_Q8_0) return k % 64 == 0 && k > 0;
+    return k % 256 == 0 && k > 0;
+}
+
+uint64_t weight_align(int fmt) { return fmt == SM_FMT_Q8_0 ? 4 : 16; }
+
+// One active byte range taking part in alias checks.
+struct Range {
+    uintptr_t ptr = 0;
+    uint64_t bytes = 0;
+    std::string name;
+    bool writable = false;
+    int stage = 0;
+};
+
+bool overlap(const Range& a, const Range& b) {
+    if (a.bytes == 0 || b.bytes == 0) return false;
+    return a.ptr < b.ptr + b.bytes && b.ptr < a.ptr + a.bytes;
+}
+
+// Validation context of one coordinator call.
+struct Check {
+    sm_context* ctx;
+    std::string prefix;  // e.g. "Prefill MoE grouping"
+    int stage = 0;
+    std::vector<Range> inputs, outputs;
+    std::string err;
+    sm_status st = SM_OK;
+
+    bool fail(sm_status s, const std::string& msg) {
+        if (st == SM_OK) { st = s; err = msg; }
+        return false;
+    }
+
+    // Resolves a view to a device address after the ownership/extent/alignment checks.
+    bool view(const sm_view& v, uint64_t need, uint64_t align, const char* name, bool writable,
+              uintptr_t& out) {
+        if (st != SM_OK) return false;
+        sm_context::Alloc a{};
+        {
+            std::lock_guard<std::mutex> lk(ctx->mu);
+            auto it = ctx->buffers.find(v.buffer);
+            if (v.buffer == 0 || it == ctx->buffers.end())
+                return fail(SM_E_OWNERSHIP, prefix + " " + name + " view is not owned by this context");
+            a = it->second;
+        }
+        uint64_t end = v.offset + v.length;
+        if (end < v.offset || end > a.bytes)
+            return fail(SM_E_VIEW, prefix + " " + name + " view is undersized or misaligned");
+        const uintptr_t p = a.ptr + v.offset;
+        if (v.length < need || align == 0 || p % align != 0)
+            return fail(SM_E_VIEW, prefix + " " + name + " view is undersized or misaligned");
+        Range r{p, need, std::string(name), writable, stage};
+        (writable ? outputs : inputs).push_back(r);
+        out = p;
+        return true;
+    }
+
+    // Outputs must be disjoint from every input and from each other
+    // (prefill_moe_grouping_dispatch.mm:234-252).
+    bool aliases() {
+        if (st != SM_OK) return false;
+        for (const auto& o : outputs)
+            for (const auto& i : inputs)
+                if (overlap(o, i)) return fail(SM_E_ALIAS, prefix + " " + o.name + " overlaps active " + i.name);
+        for (size_t i = 0; i < outputs.size(); ++i)
+            for (size_t j = i + 1; j < outputs.size(); ++j)
+                if (overlap(outputs[i], outputs[j]))
+                    return fail(SM_E_ALIAS, prefix + " " + outputs[i].name + " overlaps active " + outputs[j].name);
+        return true;
+    }
+};
+
+sm_status shape_check(const sm_moe_shape* s, const char* prefix, std::string& err, bool need_ff) {
+    if (s == nullptr) { err = std::string(prefix) + " shape is null"; return SM_E_ARGUMENT; }
+    if (s->rows == 0 || s->rows > SM_MAX_ROWS) {
+        err = std::string(prefix) + " row count exceeds the supported range";
+        return SM_E_SHAPE;
+    }
+    if (s->n_experts == 0 || s->n_experts > SM_MAX_EXPERTS) {
+        err = std::string(prefix) + " supports 1..512 experts";
+        return SM_E_SHAPE;
+    }
+    if (s->top_k == 0 || s->top_k > SM_MAX_TOP_K || s->top_k > s->n_experts) {
+        err = std::string(prefix) + " top-k must be 1..min(experts, 32)";
+        return SM_E_SHAPE;
+    }
+    if (s->hidden == 0 || s->hidden % 256 != 0) {
+        err = std::string(prefix) + " hidden width must be a positive multiple of 256";
+        return SM_E_SHAPE;
+    }
+    if (need_ff && (s->expert_ff == 0 || s->expert_ff % 64 != 0)) {
+        err = std::string(prefix) + " expert width must be a positive multiple of 64";
+        return SM_E_SHAPE;
+    }
+    return SM_OK;
+}
+
+sm_status record_fail(sm_segment* seg, sm_status st, const std::string& err) {
+    if (!seg->failed) { seg->failed = true; seg->error = err; }
+    return st;
+}
+
+void add_step(sm_segment* seg, const char* label, std::function<hipError_t(hipStream_t)> fn) {
+    seg->steps.push_back({label, std::move(fn)});
+}
+
+// ---- stage encoders (validation + deferred launches) --------------------------------
+
+struct RouteRes { uintptr_t logits, ids, weights; };
+bool check_route(Check& c, const sm_moe_shape& s, const sm_route_buffers& b, RouteRes& r, bool logits_input) {
+    uint64_t lb, ob;
+    if (!mul_ok({s.rows, s.n_experts, 4}, lb) || !mul_ok({s.rows, s.top_k, 4}, ob))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    // Logits are an input of the route stage alone, and an output of route/gather.
+    bool ok = c.view(b.logits, lb, 4, "logits", !logits_input, r.logits);
+    ok = ok && c.view(b.ids, ob, 4, "route IDs", true, r.ids) && c.view(b.weights, ob, 4, "route weights", true, r.weights);
+    return ok;
+}
+
+void encode_route_launch(sm_segment* seg, const sm_moe_shape& s, int divide, const RouteRes& r) {
+    const auto rows = s.rows, E = s.n_experts, K = s.top_k;
+    add_step(seg, "route top-k", [=](hipStream_t st) {
+        return sm::launch_route_topk(reinterpret_cast<const float*>(r.logits), reinterpret_cast<int32_t*>(r.ids),
+                                     reinterpret_cast<float*>(r.weights), rows, E, K, divide, st);
+    });
+}
+
+struct GroupRes { uintptr_t ids, mixed, hist, plan, tiles, src, dst, gathered; };
+bool check_grouping(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& b, GroupRes& r) {
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    if (N > 0x7fffffffull) return c.fail(SM_E_SHAPE, c.prefix + " entry count exceeds kernel indexing");
+    uint64_t hist_b, tiles_b, route_b, mixed_b, gath_b;
+    if (!mul_ok({ceil_div(N, SM_COUNT_TILE) + 1, s.n_experts, 4}, hist_b) ||
+        !mul_ok({ceil_div(N, SM_EXPERT_TILE) + s.n_experts, 8}, tiles_b) || !mul_ok({N, 4}, route_b) ||
+        !mul_ok({s.rows, s.hidden, 2}, mixed_b) || !mul_ok({N, s.hidden, 2}, gath_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    return c.view(b.ids, route_b, 4, "route IDs", false, r.ids) &&
+           c.view(b.mixed_h, mixed_b, 16, "mixed activation", false, r.mixed) &&
+           c.view(b.histogram, hist_b, 4, "histogram", true, r.hist) &&
+           c.view(b.plan, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", true, r.plan) &&
+           c.view(b.tiles, tiles_b, 8, "tile list", true, r.tiles) &&
+           c.view(b.source_rows, route_b, 4, "source rows", true, r.src) &&
+           c.view(b.destination_rows, route_b, 4, "destination rows", true, r.dst) &&
+           c.view(b.gathered_rows, gath_b, 16, "gathered rows", true, r.gathered);
+}
+
+void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupRes& r) {
+    const auto rows = s.rows, E = s.n_experts, K = s.top_k, d = s.hidden;
+    add_step(seg, "grouping", [=](hipStream_t st) {
+        return sm::launch_grouping(reinterpret_cast<const int32_t*>(r.ids), rows, K, E,
+                                   reinterpret_cast<uint32_t*>(r.hist), reinterpret_cast<sm::Plan*>(r.plan),
+                                   reinterpret_cast<uint32_t*>(r.tiles), reinterpret_cast<int32_t*>(r.src),
+                                   reinterpret_cast<int32_t*>(r.dst), st);
+    });
+    add_step(seg, "gather", [=](hipStream_t st) {
+        return sm::launch_gather(reinterpret_cast<const _Float16*>(r.mixed), rows, d,
+                                 reinterpret_cast<const int32_t*>(r.src), reinterpret_cast<const sm::Plan*>(r.plan),
+                                 rows * K, reinterpret_cast<_Float16*>(r.gathered), st);
+    });
+}
+
+struct RouterRes { uintptr_t x, w, bias, logits; };
+
+// Expert weight table: validates every non-null address of the used roles against the
+// declared storage (prefill_moe_expert_dispatch.mm:377-448) and snapshots the table.
+struct WeightsRes { uintptr_t snapshot; std::vector<uint64_t> table; };
+bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, int fmt, bool gate_up,
+                   WeightsRes& r) {
+    if (w.addresses == nullptr) return c.fail(SM_E_ARGUMENT, c.prefix + " address table is null");
+    const uint64_t E = s.n_experts;
+    if (!c.view(w.address_snapshot, E * 3 * 8, 8, "address snapshot", true, r.snapshot)) return false;
+    const uint64_t per_row = gate_up ? fmt_row_bytes(fmt, s.hidden) : fmt_row_bytes(fmt, s.expert_ff);
+    uint64_t expert_bytes;
+    if (!mul_ok({per_row, gate_up ? uint64_t(s.expert_ff) : uint64_t(s.hidden)}, expert_bytes) || per_row == 0)
+        return c.fail(SM_E_SHAPE, c.prefix + " expert weight extent is invalid");
+    std::vector<Range> storage;
+    for (uint32_t i = 0; i < w.n_storage; ++i) {
+        uintptr_t p;
+        const sm_view& v = w.storage[i];
+        if (!c.view(v, v.length, 1, "weight storage", false, p)) return false;
+        storage.push_back({p, v.length, "weight storage", false, c.stage});
+    }
+    r.table.assign(w.addresses, w.addresses + E * 3);
+    const uint64_t align = weight_align(fmt);
+    for (uint64_t e = 0; e < E; ++e) {
+        for (int role = 0; role < 3; ++role) {
+            if (gate_up ? role == 2 : role != 2) continue;
+            const uint64_t a = r.table[e * 3 + role];
+            if (a == 0) continue;  // reported on the GPU (status bit 0) if the expert is active
+            bool inside = false;
+            for (const auto& st : storage)
+                if (a >= st.ptr && a - st.ptr <= st.bytes && expert_bytes <= st.bytes - (a - st.ptr)) inside = true;
+            if (!inside || a % align != 0) {
+                char msg[160];
+                std::snprintf(msg, sizeof msg, " expert %llu %s address is outside declared storage or misaligned",
+                              (unsigned long long)e, role == 0 ? "gate" : (role == 1 ? "up" : "down"));
+                return c.fail(SM_E_ADDRESS, c.prefix + msg);
+            }
+        }
+    }
+    return true;
+}
+
+// Writes the validated table into the device snapshot from kernel arguments (no host
+// staging memory has to outlive the call).
+void encode_snapshot(sm_segment* seg, const WeightsRes& w);
+
+struct GateUpRes { WeightsRes w; uintptr_t xs, plan, tiles, hidden, status; };
+bool check_gate_up(Check& c, const sm_moe_shape& s, int fmt, const sm_gate_up_buffers& b, GateUpRes& r) {
+    if (!routed_fmt(fmt)) return c.fail(SM_E_FORMAT, c.prefix + " weight format is not a supported block format");
+    if (!k_ok(fmt, s.hidden) || s.expert_ff % 64 != 0)
+        return c.fail(SM_E_SHAPE, c.prefix + " widths do not fit the weight format's blocks");
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    uint64_t xs_b, h_b, tiles_b;
+    if (!mul_ok({N, s.hidden, 2}, xs_b) || !mul_ok({N, s.expert_ff, 2}, h_b) ||
+        !mul_ok({ceil_div(N, SM_EXPERT_TILE) + s.n_experts, 8}, tiles_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    return check_weights(c, s, b.weights, fmt, true, r.w) &&
+           c.view(b.gathered_rows, xs_b, 16, "gathered rows", false, r.xs) &&
+           c.view(b.plan, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", false, r.plan) &&
+           c.view(b.tiles, tiles_b, 8, "tile list", false, r.tiles) &&
+           c.view(b.hidden, h_b, 16, "hidden", true, r.hidden) &&
+           c.view(b.status, 4, 4, "status", true, r.status);
+}
+
+void encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r) {
+    encode_snapshot(seg, r.w);
+    const uint32_t N = s.rows * s.top_k;
+    const uint32_t cap = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
+    sm::RoutedGemm g{};
+    g.addresses = reinterpret_cast<const uint64_t*>(r.w.snapshot);
+    g.a = reinterpret_cast<const _Float16*>(r.xs);
+    g.plan = reinterpret_cast<const sm::Plan*>(r.plan);
+    g.tiles = reinterpret_cast<const uint32_t*>(r.tiles);
+    g.out_h = reinterpret_cast<_Float16*>(r.hidden);
+    g.status = reinterpret_cast<uint32_t*>(r.status);
+    g.n_entries = N;
+    g.n_experts = s.n_experts;
+    g.tile_capacity = cap;
+    g.k = s.hidden;
+    g.n_out = s.expert_ff;
+    g.row_bytes = fmt_row_bytes(fmt, s.hidden);
+    const uint32_t E = s.n_experts;
+    add_step(seg, "gate/up plan validate", [=](hipStream_t st) {
+        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, st);
+    });
+    add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fmt), g, st); });
+}
+
+struct DownRes { WeightsRes w; uintptr_t hidden, plan, tiles, dst, parts, status; };
+bool check_down(Check& c, const sm_moe_shape& s, int fmt, const sm_down_buffers& b, DownRes& r) {
+    if (!routed_fmt(fmt)) return c.fail(SM_E_FORMAT, c.prefix + " weight format is not a supported block format");
+    if (!k_ok(fmt, s.expert_ff) || s.hidden % 128 != 0)
+        return c.fail(SM_E_SHAPE, c.prefix + " widths do not fit the weight format's blocks");
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    uint64_t h_b, p_b, tiles_b;
+    if (!mul_ok({N, s.expert_ff, 2}, h_b) || !mul_ok({N, s.hidden, 4}, p_b) ||
+        !mul_ok({ceil_div(N, SM_EXPERT_TILE) + s.n_experts, 8}, tiles_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    return check_weights(c, s, b.weights, fmt, false, r.w) &&
+           c.view(b.hidden, h_b, 16, "hidden", false, r.hidden) &&
+           c.view(b.plan, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", false, r.plan) &&
+           c.view(b.tiles, tiles_b, 8, "tile list", false, r.tiles) &&
+           c.view(b.destinations, N * 4, 4, "destinations", false, r.dst) &&
+           c.view(b.parts, p_b, 16, "parts", true, r.parts) &&
+           c.view(b.status, 4, 4, "status", true, r.status);
+}
+
+void encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r) {
+    encode_snapshot(seg, r.w);
+    const uint32_t N = s.rows * s.top_k;
+    const uint32_t cap = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
+    sm::RoutedGemm g{};
+    g.addresses = reinterpret_cast<const uint64_t*>(r.w.snapshot);
+    g.a = reinterpret_cast<const _Float16*>(r.hidden);
+    g.plan = reinterpret_cast<const sm::Plan*>(r.plan);
+    g.tiles = reinterpret_cast<const uint32_t*>(r.tiles);
+    g.dst = reinterpret_cast<const int32_t*>(r.dst);
+    g.out_f = reinterpret_cast<float*>(r.parts);
+    g.status = reinterpret_cast<uint32_t*>(r.status);
+    g.n_entries = N;
+    g.n_experts = s.n_experts;
+    g.tile_capacity = cap;
+    g.k = s.expert_ff;
+    g.n_out = s.hidden;
+    g.row_bytes = fmt_row_bytes(fmt, s.expert_ff);
+    const uint32_t E = s.n_experts;
+    add_step(seg, "down plan validate", [=](hipStream_t st) {
+        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, st);
+    });
+    // The destination bitset borrows the head of `parts`, which the down tiles overwrite
+    // (the reference's prefill_moe_down_dispatch.mm:470-520 does the same).
+    add_step(seg, "down destination validate", [=](hipStream_t st) {
+        return sm::launch_destination_validate(g.dst, reinterpret_cast<uint32_t*>(g.out_f), g.status, N, st);
+    });
+    add_step(seg, "down tiles", [=](hipStream_t st) { return sm::launch_down(Fmt(fmt), g, st); });
+}
+
+struct SharedRes { uintptr_t x, wg, wu, wd, gv, hidden, out, gl; };
+bool check_shared(Check& c, const sm_moe_shape& s, int fmt, const sm_shared_buffers& b, SharedRes& r) {
+    if (!dense_fmt(fmt)) return c.fail(SM_E_FORMAT, c.prefix + " shared expert format must be F16 or BF16");
+    const uint64_t Is = s.shared_ff;
+    if (Is == 0 || Is % 256 != 0 || s.hidden % 128 != 0)
+        return c.fail(SM_E_SHAPE, c.prefix + " shared expert width must be a positive multiple of 256");
+    uint64_t x_b, w_b, h_b, o_b;
+    if (!mul_ok({s.rows, s.hidden, 2}, x_b) || !mul_ok({Is, s.hidden, 2}, w_b) || !mul_ok({s.rows, Is, 2}, h_b) ||
+        !mul_ok({s.rows, s.hidden, 4}, o_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    return c.view(b.mixed_h, x_b, 16, "mixed activation", false, r.x) &&
+           c.view(b.gate_weights, w_b, 16, "gate weights", false, r.wg) &&
+           c.view(b.up_weights, w_b, 16, "up weights", false, r.wu) &&
+           c.view(b.down_weights, w_b, 16, "down weights", false, r.wd) &&
+           c.view(b.gate_vector, uint64_t(s.hidden) * 2, 2, "gate vector", false, r.gv) &&
+           c.view(b.hidden, h_b, 16, "hidden", true, r.hidden) &&
+           c.view(b.output, o_b, 16, "output", true, r.out) &&
+           c.view(b.gate_logit, uint64_t(s.rows) * 4, 4, "gate logit", true, r.gl);
+}
+
+void encode_shared_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r) {
+    sm::DenseGemm gu{};
+    gu.a = reinterpret_cast<const _Float16*>(r.x);
+    gu.w0 = reinterpret_cast<const uint8_t*>(r.wg);
+    gu.w1 = reinterpret_cast<const uint8_t*>(r.wu);
+    gu.out_h = reinterpret_cast<_Float16*>(r.hidden);
+    gu.rows = s.rows;
+    gu.k = s.hidden;
+    gu.n_out = s.shared_ff;
+    gu.row_bytes = 2ull * s.hidden;
+    sm::DenseGemm dn{};
+    dn.a = reinterpret_cast<const _Float16*>(r.hidden);
+    dn.w0 = reinterpret_cast<const uint8_t*>(r.wd);
+    dn.out_f = reinterpret_cast<float*>(r.out);
+    dn.rows = s.rows;
+    dn.k = s.shared_ff;
+    dn.n_out = s.hidden;
+    dn.row_bytes = 2ull * s.shared_ff;
+    const auto rows = s.rows, d = s.hidden;
+    const uintptr_t x = r.x, gv = r.gv, gl = r.gl;
+    add_step(seg, "shared gate/up", [=](hipStream_t st) { return sm::launch_dense_gate_up(Fmt(fmt), gu, st); });
+    add_step(seg, "shared down", [=](hipStream_t st) { return sm::launch_dense_down(Fmt(fmt), dn, st); });
+    add_step(seg, "shared gate logit", [=](hipStream_t st) {
+        return sm::launch_gate_logit(Fmt(fmt), reinterpret_cast<const _Float16*>(x), reinterpret_cast<const uint8_t*>(gv),
+                                     reinterpret_cast<float*>(gl), rows, d, st);
+    });
+}
+
+struct CombineRes { uintptr_t parts, weights, shared, gate, out; };
+bool check_combine(Check& c, const sm_moe_shape& s, const sm_combine_buffers& b, CombineRes& r) {
+    if (s.hidden % 4 != 0) return c.fail(SM_E_SHAPE, c.prefix + " hidden width must be a multiple of 4");
+    uint64_t p_b, w_b, o_b;
+    if (!mul_ok({s.rows, s.top_k, s.hidden, 4}, p_b) || !mul_ok({s.rows, s.top_k, 4}, w_b) ||
+        !mul_ok({s.rows, s.hidden, 4}, o_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    r.shared = r.gate = 0;
+    bool ok = c.view(b.parts, p_b, 16, "parts", false, r.parts) && c.view(b.weights, w_b, 4, "weights", false, r.weights);
+    if (ok && s.shared_ff != 0)
+        ok = c.view(b.shared, o_b, 16, "shared", false, r.shared) &&
+             c.view(b.gate, uint64_t(s.rows) * 4, 4, "gate", false, r.gate);
+    return ok && c.view(b.output, o_b, 16, "output", true, r.out);
+}
+
+void encode_combine_launch(sm_segment* seg, const sm_moe_shape& s, const CombineRes& r) {
+    const auto rows = s.rows, K = s.top_k, d = s.hidden;
+    add_step(seg, "combine", [=](hipStream_t st) {
+        return sm::launch_combine(reinterpret_cast<const float*>(r.parts), reinterpret_cast<const float*>(r.weights),
+                                  reinterpret_cast<const float*>(r.shared), reinterpret_cast<const float*>(r.gate),
+                                  reinterpret_cast<float*>(r.out), rows, K, d, st);
+    });
+}
+
+sm_status begin_check(sm_segment* seg, const char* prefix, Check& c) {
+    if (seg == nullptr) return SM_E_ARGUMENT;
+    c.ctx = seg->ctx;
+    c.prefix = prefix;
+    if (seg->failed) return SM_E_SEGMENT;
+    return SM_OK;
+}
+
+sm_status finish(sm_segment* seg, Check& c) {
+    if (c.st != SM_OK) return record_fail(seg, c.st, c.err);
+    return SM_OK;
+}
+
+// Cross-stage dataflow edges a full layer may alias (prefill_moe_full_pipeline.cpp:109-162):
+// a writer and a reader of a later stage may share memory only on these edges, and only
+// when they start at the same address and the reader lies inside the writer.
+bool expected_edge(const Range& w, const Range& r) {
+    static const char* const edges[][2] = {
+        {"route.gathered rows", "gate_up.gathered rows"}, {"route.PfPlan slot", "gate_up.PfPlan slot"},
+        {"route.PfPlan slot", "down.PfPlan slot"},       {"route.tile list", "gate_up.tile list"},
+        {"route.tile list", "down.tile list"},           {"route.destination rows", "down.destinations"},
+        {"route.route weights", "combine.weights"},      {"shared.output", "combine.shared"},
+        {"shared.gate logit", "combine.gate"},           {"gate_up.hidden", "down.hidden"},
+        {"down.parts", "combine.parts"},
+    };
+    if (!w.writable || r.writable || w.stage >= r.stage) return false;
+    for (const auto& e : edges)
+        if (w.name == e[0] && r.name == e[1]) return w.ptr == r.ptr && r.bytes <= w.bytes;
+    return false;
+}
+
+}  // namespace
+
+// Snapshot kernel: one launch per 320 table words.
+struct SnapChunk { uint64_t v[320]; };
+__global__ void snapshot_write_kernel(uint64_t* dst, uint32_t count, SnapChunk chunk) {
+    const uint32_t i = threadIdx.x;
+    if (i < count) dst[i] = chunk.v[i];
+}
+
+namespace {
+void encode_snapshot(sm_segment* seg, const WeightsRes& w) {
+    const uint64_t words = w.table.size();
+    for (uint64_t base = 0; base < words; base += 320) {
+        SnapChunk ch{};
+        const uint32_t count = uint32_t(std::min<uint64_t>(320, words - base));
+        std::memcpy(ch.v, w.table.data() + base, count * 8);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(w.snapshot) + base;
+        add_step(seg, "address snapshot", [=](hipStream_t st) {
+            snapshot_write_kernel<<<1, 320, 0, st>>>(dst, count, ch);
+            return hipGetLastError();
+        });
+    }
+}
+}  // namespace
+
+extern "C" {
+
+uint32_t sm_abi_version(void) { return SM_ABI_VERSION; }
+
+uint64_t sm_histogram_bytes(const sm_moe_shape* s) {
+    if (!s) return 0;
+    const uint64_t N = uint64_t(s->rows) * s->top_k;
+    return (ceil_div(N, SM_COUNT_TILE) + 1) * s->n_experts * 4;
+}
+uint64_t sm_tiles_bytes(const sm_moe_shape* s) {
+    if (!s) return 0;
+    const uint64_t N = uint64_t(s->rows) * s->top_k;
+    return (ceil_div(N, SM_EXPERT_TILE) + s->n_experts) * 8;
+}
+uint64_t sm_format_row_bytes(sm_format fmt, uint64_t values) { return fmt_row_bytes(fmt, values); }
+
+sm_status sm_context_create(int device, sm_context** out) {
+    if (out == nullptr || device < 0) return SM_E_ARGUMENT;
+    // A context without a visible device still validates and encodes (host-only use,
+    // e.g. preflight tests); commit then reports SM_E_DEVICE.
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    if (n > 0 && device >= n) return SM_E_DEVICE;
+    auto* c = new (std::nothrow) sm_context();
+    if (!c) return SM_E_DEVICE;
+    c->device = device;
+    c->has_device = n > 0;
+    *out = c;
+    return SM_OK;
+}
+
+void sm_context_destroy(sm_context* ctx) { delete ctx; }
+
+sm_status sm_buffer_register(sm_context* ctx, void* ptr, uint64_t bytes, uint64_t* handle) {
+    if (!ctx || !ptr || !handle || bytes == 0) return SM_E_ARGUMENT;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const uint64_t h = ctx->next_handle++;
+    ctx->buffers[h] = {reinterpret_cast<uintptr_t>(ptr), bytes};
+    *handle = h;
+    return SM_OK;
+}
+
+sm_status sm_buffer_unregister(sm_context* ctx, uint64_t handle) {
+    if (!ctx) return SM_E_ARGUMENT;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return ctx->buffers.erase(handle) ? SM_OK : SM_E_OWNERSHIP;
+}
+
+sm_status sm_segment_begin(sm_context* ctx, sm_segment** out) {
+    if (!ctx || !out) return SM_E_ARGUMENT;
+    auto* s = new (std::nothrow) sm_segment();
+    if (!s) return SM_E_DEVICE;
+    s->ctx = ctx;
+    *out = s;
+    return SM_OK;
+}
+
+sm_status sm_segment_commit(sm_segment* seg, void* stream) {
+    if (!seg) return SM_E_ARGUMENT;
+    if (seg->failed) { delete seg; return SM_E_SEGMENT; }
+    sm_status st = SM_OK;
+    if (!seg->ctx->has_device || hipSetDevice(seg->ctx->device) != hipSuccess) st = SM_E_DEVICE;
+    for (auto& step : seg->steps) {
+        if (st != SM_OK) break;
+        if (step.run(reinterpret_cast<hipStream_t>(stream)) != hipSuccess) st = SM_E_DEVICE;
+    }
+    delete seg;
+    return st;
+}
+
+void sm_segment_abort(sm_segment* seg) { delete seg; }
+
+const char* sm_segment_error(const sm_segment* seg) { return seg ? seg->error.c_str() : ""; }
+uint32_t sm_segment_launches(const sm_segment* seg) { return seg ? uint32_t(seg->steps.size()) : 0; }
+
+sm_status sm_encode_route(sm_segment* seg, const sm_moe_shape* shape, int divide, const sm_route_buffers* b) {
+    Check c;
+    sm_status st = begin_check(seg, "MoE route", c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, "MoE route", err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, "MoE route buffers are null");
+    RouteRes r{};
+    if (!check_route(c, *shape, *b, r, true) || !c.aliases()) return finish(seg, c);
+    encode_route_launch(seg, *shape, divide, r);
+    return SM_OK;
+}
+
+sm_status sm_encode_grouping(sm_segment* seg, const sm_moe_shape* shape, const sm_grouping_buffers* b) {
+    Check c;
+    sm_status st = begin_check(seg, "Prefill MoE grouping", c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, "Prefill MoE grouping", err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, "Prefill MoE grouping buffers are null");
+    GroupRes r{};
+    if (!check_grouping(c, *shape, *b, r) || !c.aliases()) return finish(seg, c);
+    encode_grouping_launch(seg, *shape, r);
+    return SM_OK;
+}
+
+namespace {
+// Validates the route+gather composition and returns its ranges (stage-tagged "route.").
+bool check_route_gather(Check& c, const sm_moe_shape& s, const sm_route_gather_buffers& b, RouterRes& rr,
+                        RouteRes& ro, GroupRes& gr) {
+    uint64_t x_b, w_b;
+    if (!mul_ok({s.rows, s.hidden, 2}, x_b) || !mul_ok({s.n_experts, s.hidden, 4}, w_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    if (!c.view(b.mixed_h, x_b, 16, "mixed activation", false, rr.x) ||
+        !c.view(b.router_weights, w_b, 16, "router weights", false, rr.w))
+        return false;
+    rr.bias = 0;
+    if (b.router_bias.buffer != 0 && !c.view(b.router_bias, uint64_t(s.n_experts) * 4, 4, "router bias", false, rr.bias))
+        return false;
+    sm_route_buffers rb{b.logits, b.route_ids, b.route_weights};
+    if (!check_route(c, s, rb, ro, false)) return false;
+    rr.logits = ro.logits;
+    // Grouping reads the IDs the route step writes; validate its other views.
+    sm_grouping_buffers gb{b.route_ids, b.mixed_h, b.histogram, b.plan, b.tiles, b.source_rows,
+                           b.destination_rows, b.gathered_rows};
+    const size_t n_in = c.inputs.size();
+    if (!check_grouping(c, s, gb, gr)) return false;
+    // Drop the duplicate input entries (route IDs and mixed activation are produced or
+    // already listed by this composition).
+    c.inputs.erase(c.inputs.begin() + n_in, c.inputs.begin() + n_in + 2);
+    return true;
+}
+
+void encode_route_gather_launch(sm_segment* seg, const sm_moe_shape& s, const RouterRes& rr, const RouteRes& ro,
+                                const GroupRes& gr) {
+    const auto rows = s.rows, d = s.hidden, E = s.n_experts;
+    add_step(seg, "router GEMM", [=](hipStream_t st) {
+        return sm::launch_router_gemm(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
+                                      reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits),
+                                      rows, d, E, st);
+    });
+    encode_route_launch(seg, s, 1, ro);
+    encode_grouping_launch(seg, s, gr);
+}
+}  // namespace
+
+sm_status sm_encode_route_gather(sm_segment* seg, const sm_moe_shape* shape, const sm_route_gather_buffers* b) {
+    Check c;
+    const char* P = "Prefill MoE route/gather";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, P, err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    RouterRes rr{};
+    RouteRes ro{};
+    GroupRes gr{};
+    if (!check_route_gather(c, *shape, *b, rr, ro, gr) || !c.aliases()) return finish(seg, c);
+    encode_route_gather_launch(seg, *shape, rr, ro, gr);
+    return SM_OK;
+}
+
+sm_status sm_encode_shared_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt, const sm_shared_buffers* b) {
+    Check c;
+    const char* P = "Prefill MoE shared FFN";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, P, err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    SharedRes r{};
+    if (!check_shared(c, *shape, fmt, *b, r) || !c.aliases()) return finish(seg, c);
+    encode_shared_launch(seg, *shape, fmt, r);
+    return SM_OK;
+}
+
+sm_status sm_encode_gate_up(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt, const sm_gate_up_buffers* b) {
+    Check c;
+    const char* P = "Prefill MoE gate/up";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, P, err, true)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    GateUpRes r{};
+    if (!check_gate_up(c, *shape, fmt, *b, r) || !c.aliases()) return finish(seg, c);
+    encode_gate_up_launch(seg, *shape, fmt, r);
+    return SM_OK;
+}
+
+sm_status sm_encode_down(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt, const sm_down_buffers* b) {
+    Check c;
+    const char* P = "Prefill MoE down";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, P, err, true)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    DownRes r{};
+    if (!check_down(c, *shape, fmt, *b, r) || !c.aliases()) return finish(seg, c);
+    encode_down_launch(seg, *shape, fmt, r);
+    return SM_OK;
+}
+
+sm_status sm_encode_swiglu(sm_segment* seg, uint32_t rows, uint32_t width, const sm_swiglu_buffers* b) {
+    Check c;
+    const char* P = "Prefill MoE SwiGLU";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    if (rows == 0 || rows > SM_MAX_ROWS || width == 0)
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " row count exceeds the supported range");
+    uint64_t n, f_b, h_b;
+    if (!mul_ok({rows, width}, n) || !mul_ok({n, 4}, f_b) || !mul_ok({n, 2}, h_b))
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " buffer size overflows");
+    uintptr_t g, u, o;
+    // Read-only inputs may alias each other; the output must be disjoint from both.
+    if (!c.view(b->gate, f_b, 4, "gate", false, g) || !c.view(b->up, f_b, 4, "up", false, u) ||
+        !c.view(b->output, h_b, 2, "output", true, o) || !c.aliases())
+        return finish(seg, c);
+    add_step(seg, "swiglu", [=](hipStream_t s) {
+        return sm::launch_swiglu(reinterpret_cast<const float*>(g), reinterpret_cast<const float*>(u),
+                                 reinterpret_cast<_Float16*>(o), n, s);
+    });
+    return SM_OK;
+}
+
+sm_status sm_encode_combine(sm_segment* seg, const sm_moe_shape* shape, const sm_combine_buffers* b) {
+    Check c;
+    const char* P = "Prefill MoE combine";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = shape_check(shape, P, err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    CombineRes r{};
+    if (!check_combine(c, *shape, *b, r) || !c.aliases()) return finish(seg, c);
+    encode_combine_launch(seg, *shape, r);
+    return SM_OK;
+}
+
+sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
+                               const sm_layer_buffers* b) {
+    const char* P = "full-mode Prefill MoE";
+    if (seg == nullptr) return SM_E_ARGUMENT;
+    if (seg->failed) return SM_E_SEGMENT;
+    std::string err;
+    sm_status st = shape_check(shape, P, err, true);
+    if (st != SM_OK) return record_fail(seg, st, err);
+    if (!b || !f) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    const sm_moe_shape& s = *shape;
+    const bool has_shared = s.shared_ff != 0;
+    // Validate every stage before anything is recorded.
+    Check cr, cs, cg, cd, cc;
+    for (Check* c : {&cr, &cs, &cg, &cd, &cc}) { c->ctx = seg->ctx; c->prefix = P; }
+    cr.stage = 0; cs.stage = 1; cg.stage = 2; cd.stage = 3; cc.stage = 4;
+    RouterRes rr{};
+    RouteRes ro{};
+    GroupRes gr{};
+    SharedRes sr{};
+    GateUpRes gu{};
+    DownRes dn{};
+    CombineRes co{};
+    const bool ok = check_route_gather(cr, s, b->route_gather, rr, ro, gr) && cr.aliases() &&
+                    (!has_shared || (check_shared(cs, s, f->shared, b->shared, sr) && cs.aliases())) &&
+                    check_gate_up(cg, s, f->gate_up, b->gate_up, gu) && cg.aliases() &&
+                    check_down(cd, s, f->down, b->down, dn) && cd.aliases() &&
+                    check_combine(cc, s, b->combine, co) && cc.aliases();
+    if (!ok) {
+        for (Check* c : {&cr, &cs, &cg, &cd, &cc})
+            if (c->st != SM_OK) return record_fail(seg, c->st, c->err);
+        return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " validation failed");
+    }
+    // Cross-stage aliasing: only the listed producer -> consumer edges.
+    std::vector<Range> all;
+    const char* names[] = {"route.", "shared.", "gate_up.", "down.", "combine."};
+    for (Check* c : {&cr, &cs, &cg, &cd, &cc}) {
+        for (auto r : c->inputs) { r.name = names[c->stage] + r.name; all.push_back(r); }
+        for (auto r : c->outputs) { r.name = names[c->stage] + r.name; all.push_back(r); }
+    }
+    for (size_t i = 0; i < all.size(); ++i)
+        for (size_t j = i + 1; j < all.size(); ++j) {
+            const Range& a = all[i];
+            const Range& bb = all[j];
+            if (a.stage == bb.stage || !overlap(a, bb) || (!a.writable && !bb.writable)) continue;
+            const Range& w = a.writable ? a : bb;
+            const Range& r = a.writable ? bb : a;
+            if (expected_edge(w, r)) continue;
+            return record_fail(seg, SM_E_ALIAS, std::string(P) + " " + w.name + " overlaps active " + r.name);
+        }
+    encode_route_gather_launch(seg, s, rr, ro, gr);
+    if (has_shared) encode_shared_launch(seg, s, f->shared, sr);
+    encode_gate_up_launch(seg, s, f->gate_up, gu);
+    encode_down_launch(seg, s, f->down, dn);
+    encode_combine_launch(seg, s, co);
+    return SM_OK;
+}
+
+// ---- standalone transactional forms --------------------------------------------------
+
+#define SM_SUBMIT_BODY(ENCODE_CALL)                                                   \
+    sm_segment* seg = nullptr;                                                        \
+    sm_status st = sm_segment_begin(ctx, &seg);                                       \
+    if (st != SM_OK) return st;                                                       \
+    st = ENCODE_CALL;                                                                 \
+    if (st != SM_OK) {                                                                \
+        if (err && cap) std::snprintf(err, cap, "%s", seg->error.c_str());            \
+        sm_segment_abort(seg);                                                        \
+        return st;                                                                    \
+    }                                                                                 \
+    st = sm_segment_commit(seg, stream);                                              \
+    if (st != SM_OK && err && cap) std::snprintf(err, cap, "HIP launch failed");      \
+    else if (err && cap) err[0] = 0;                                                  \
+    return st;
+
+sm_status sm_submit_route(sm_context* ctx, void* stream, const sm_moe_shape* shape, int divide,
+                          const sm_route_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_route(seg, shape, divide, b))
+}
+sm_status sm_submit_grouping(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                             const sm_grouping_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_grouping(seg, shape, b))
+}
+sm_status sm_submit_route_gather(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                                 const sm_route_gather_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_route_gather(seg, shape, b))
+}
+sm_status sm_submit_shared_ffn(sm_context* ctx, void* stream, const sm_moe_shape* shape, sm_format fmt,
+                               const sm_shared_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_shared_ffn(seg, shape, fmt, b))
+}
+sm_status sm_submit_gate_up(sm_context* ctx, void* stream, const sm_moe_shape* shape, sm_format fmt,
+                            const sm_gate_up_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_gate_up(seg, shape, fmt, b))
+}
+sm_status sm_submit_down(sm_context* ctx, void* stream, const sm_moe_shape* shape, sm_format fmt,
+                         const sm_down_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_down(seg, shape, fmt, b))
+}
+sm_status sm_submit_swiglu(sm_context* ctx, void* stream, uint32_t rows, uint32_t width,
+                           const sm_swiglu_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_swiglu(seg, rows, width, b))
+}
+sm_status sm_submit_combine(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                            const sm_combine_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_combine(seg, shape, b))
+}
+sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                               const sm_layer_formats* formats, const sm_layer_buffers* b, char* err,
+                               size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_full_layer(seg, shape, formats, b))
+}
+
+sm_status sm_read_layer_status(sm_context* ctx, void* stream, sm_view plan, sm_view gu, sm_view dn,
+                               uint32_t* bad, uint32_t* gu_bits, uint32_t* dn_bits) {
+    if (!ctx) return SM_E_ARGUMENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return SM_E_DEVICE;
+    if (hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)) != hipSuccess) return SM_E_DEVICE;
+    auto read_word = [&](const sm_view& v, uint64_t off, uint32_t* out) -> sm_status {
+        if (!out) return SM_OK;
+        *out = 0;
+        if (v.buffer == 0) return SM_OK;
+        sm_context::Alloc a{};
+        {
+            std::lock_guard<std::mutex> lk(ctx->mu);
+            auto it = ctx->buffers.find(v.buffer);
+            if (it == ctx->buffers.end()) return SM_E_OWNERSHIP;
+            a = it->second;
+        }
+        if (v.offset + off + 4 > a.bytes || v.length < off + 4) return SM_E_VIEW;
+        if (hipMemcpy(out, reinterpret_cast<void*>(a.ptr + v.offset + off), 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return SM_E_DEVICE;
+        return SM_OK;
+    };
+    sm_status st = read_word(plan, 20, bad);  // PfPlan.bad
+    if (st == SM_OK) st = read_word(gu, 0, gu_bits);
+    if (st == SM_OK) st = read_word(dn, 0, dn_bits);
+    return st;
+}
+
+}  // extern "C"

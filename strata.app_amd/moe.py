@@ -1,0 +1,370 @@
+"""Python host mirror of the Prefill MoE coordinators over libstrata_moe.so.
+
+Names, argument meaning and error behaviour follow the reference's C++ coordinators in
+namespace strata::metal (include/strata/metal/prefill_moe_*.hpp): every ``encode_*`` call
+returns ``(ok, error)`` like the reference's ``bool`` + ``std::string& error``; a failed
+encode poisons the segment, which must then be aborted (the reference's "propagate false so
+the whole segment is discarded"). Device memory is plain torch tensors registered with a
+``Context``; the library itself never allocates on the layer path.
+
+The HIP library is required: importing this module on a machine without the built
+``libstrata_moe.so`` raises, and there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+from typing import Optional, Sequence
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libstrata_moe.so"
+
+# ---- formats / status (include/strata_moe.h) -------------------------------------------
+Q8_0, Q4_K, Q2_K, F16, BF16 = 1, 2, 3, 4, 5
+FORMAT_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q2_K: "Q2_K", F16: "F16", BF16: "BF16"}
+STATUS_NAMES = {
+    0: "SM_OK", 1: "SM_E_ARGUMENT", 2: "SM_E_SHAPE", 3: "SM_E_VIEW", 4: "SM_E_OWNERSHIP",
+    5: "SM_E_ALIAS", 6: "SM_E_SEGMENT", 7: "SM_E_FORMAT", 8: "SM_E_ADDRESS", 9: "SM_E_DEVICE",
+}
+PLAN_BYTES = 6180
+PLAN_SLOT_BYTES = 6400
+COUNT_TILE = 256
+EXPERT_TILE = 64
+
+# The C ABI's exported symbols; tests check the library exports each one.
+EXPORTS = (
+    "sm_abi_version", "sm_histogram_bytes", "sm_tiles_bytes", "sm_format_row_bytes",
+    "sm_context_create", "sm_context_destroy", "sm_buffer_register", "sm_buffer_unregister",
+    "sm_segment_begin", "sm_segment_commit", "sm_segment_abort", "sm_segment_error",
+    "sm_segment_launches",
+    "sm_encode_route", "sm_encode_grouping", "sm_encode_route_gather", "sm_encode_shared_ffn",
+    "sm_encode_gate_up", "sm_encode_down", "sm_encode_swiglu", "sm_encode_combine",
+    "sm_encode_full_layer",
+    "sm_submit_route", "sm_submit_grouping", "sm_submit_route_gather", "sm_submit_shared_ffn",
+    "sm_submit_gate_up", "sm_submit_down", "sm_submit_swiglu", "sm_submit_combine",
+    "sm_submit_full_layer", "sm_read_layer_status",
+    "sm_synth_normal_f32", "sm_synth_normal_f16", "sm_synth_normal_bf16", "sm_quantize",
+    "sm_synth_quantized",
+)
+
+
+class View(C.Structure):
+    _fields_ = [("buffer", C.c_uint64), ("offset", C.c_uint64), ("length", C.c_uint64)]
+
+
+NULL_VIEW = View(0, 0, 0)
+
+
+class Shape(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("hidden", C.c_uint32), ("n_experts", C.c_uint32),
+                ("top_k", C.c_uint32), ("expert_ff", C.c_uint32), ("shared_ff", C.c_uint32)]
+
+
+class RouteBuffers(C.Structure):
+    _fields_ = [("logits", View), ("ids", View), ("weights", View)]
+
+
+class GroupingBuffers(C.Structure):
+    _fields_ = [("ids", View), ("mixed_h", View), ("histogram", View), ("plan", View),
+                ("tiles", View), ("source_rows", View), ("destination_rows", View),
+                ("gathered_rows", View)]
+
+
+class RouteGatherBuffers(C.Structure):
+    _fields_ = [("mixed_h", View), ("router_weights", View), ("logits", View),
+                ("route_ids", View), ("route_weights", View), ("histogram", View),
+                ("plan", View), ("tiles", View), ("source_rows", View),
+                ("destination_rows", View), ("gathered_rows", View), ("router_bias", View)]
+
+
+class ExpertWeights(C.Structure):
+    _fields_ = [("addresses", C.POINTER(C.c_uint64)), ("address_snapshot", View),
+                ("storage", C.POINTER(View)), ("n_storage", C.c_uint32)]
+
+
+class GateUpBuffers(C.Structure):
+    _fields_ = [("weights", ExpertWeights), ("gathered_rows", View), ("plan", View),
+                ("tiles", View), ("hidden", View), ("status", View)]
+
+
+class DownBuffers(C.Structure):
+    _fields_ = [("weights", ExpertWeights), ("hidden", View), ("plan", View), ("tiles", View),
+                ("destinations", View), ("parts", View), ("status", View)]
+
+
+class SharedBuffers(C.Structure):
+    _fields_ = [("mixed_h", View), ("gate_weights", View), ("up_weights", View),
+                ("down_weights", View), ("gate_vector", View), ("hidden", View),
+                ("output", View), ("gate_logit", View)]
+
+
+class SwiGLUBuffers(C.Structure):
+    _fields_ = [("gate", View), ("up", View), ("output", View)]
+
+
+class CombineBuffers(C.Structure):
+    _fields_ = [("parts", View), ("weights", View), ("shared", View), ("gate", View),
+                ("output", View)]
+
+
+class LayerFormats(C.Structure):
+    _fields_ = [("gate_up", C.c_int), ("down", C.c_int), ("shared", C.c_int)]
+
+
+class LayerBuffers(C.Structure):
+    _fields_ = [("route_gather", RouteGatherBuffers), ("shared", SharedBuffers),
+                ("gate_up", GateUpBuffers), ("down", DownBuffers),
+                ("combine", CombineBuffers)]
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def library() -> C.CDLL:
+    """Loads libstrata_moe.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    lib = C.CDLL(str(LIB_PATH))
+    P, U32, U64, I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
+    sig = {
+        "sm_abi_version": (U32, []),
+        "sm_histogram_bytes": (U64, [C.POINTER(Shape)]),
+        "sm_tiles_bytes": (U64, [C.POINTER(Shape)]),
+        "sm_format_row_bytes": (U64, [I, U64]),
+        "sm_context_create": (I, [I, C.POINTER(P)]),
+        "sm_context_destroy": (None, [P]),
+        "sm_buffer_register": (I, [P, P, U64, C.POINTER(U64)]),
+        "sm_buffer_unregister": (I, [P, U64]),
+        "sm_segment_begin": (I, [P, C.POINTER(P)]),
+        "sm_segment_commit": (I, [P, P]),
+        "sm_segment_abort": (None, [P]),
+        "sm_segment_error": (C.c_char_p, [P]),
+        "sm_segment_launches": (U32, [P]),
+        "sm_encode_route": (I, [P, C.POINTER(Shape), I, C.POINTER(RouteBuffers)]),
+        "sm_encode_grouping": (I, [P, C.POINTER(Shape), C.POINTER(GroupingBuffers)]),
+        "sm_encode_route_gather": (I, [P, C.POINTER(Shape), C.POINTER(RouteGatherBuffers)]),
+        "sm_encode_shared_ffn": (I, [P, C.POINTER(Shape), I, C.POINTER(SharedBuffers)]),
+        "sm_encode_gate_up": (I, [P, C.POINTER(Shape), I, C.POINTER(GateUpBuffers)]),
+        "sm_encode_down": (I, [P, C.POINTER(Shape), I, C.POINTER(DownBuffers)]),
+        "sm_encode_swiglu": (I, [P, U32, U32, C.POINTER(SwiGLUBuffers)]),
+        "sm_encode_combine": (I, [P, C.POINTER(Shape), C.POINTER(CombineBuffers)]),
+        "sm_encode_full_layer": (I, [P, C.POINTER(Shape), C.POINTER(LayerFormats),
+                                     C.POINTER(LayerBuffers)]),
+        "sm_submit_full_layer": (I, [P, P, C.POINTER(Shape), C.POINTER(LayerFormats),
+                                     C.POINTER(LayerBuffers), C.c_char_p, C.c_size_t]),
+        "sm_read_layer_status": (I, [P, P, View, View, View, C.POINTER(U32), C.POINTER(U32),
+                                     C.POINTER(U32)]),
+        "sm_synth_normal_f32": (None, [U64, U64, C.c_float, P, U64]),
+        "sm_synth_normal_f16": (None, [U64, U64, C.c_float, P, U64]),
+        "sm_synth_normal_bf16": (None, [U64, U64, C.c_float, P, U64]),
+        "sm_quantize": (I, [I, P, U64, U64, P]),
+        "sm_synth_quantized": (I, [I, U64, U64, C.c_float, U64, U64, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def row_bytes(fmt: int, values: int) -> int:
+    return int(library().sm_format_row_bytes(fmt, values))
+
+
+def histogram_bytes(shape: Shape) -> int:
+    return int(library().sm_histogram_bytes(C.byref(shape)))
+
+
+def tiles_bytes(shape: Shape) -> int:
+    return int(library().sm_tiles_bytes(C.byref(shape)))
+
+
+class Buffer:
+    """A device allocation registered with a Context (the reference's BufferRef owner)."""
+
+    def __init__(self, ctx: "Context", tensor, handle: int):
+        self.ctx, self.tensor, self.handle = ctx, tensor, handle
+        self.nbytes = tensor.numel() * tensor.element_size()
+
+    @property
+    def ptr(self) -> int:
+        return self.tensor.data_ptr()
+
+    def view(self, offset: int = 0, length: Optional[int] = None) -> View:
+        return View(self.handle, offset, self.nbytes - offset if length is None else length)
+
+
+class Context:
+    """Owns the allocation registry that backs the 'owned by this context' checks."""
+
+    def __init__(self, device: int = 0):
+        self.lib = library()
+        h = C.c_void_p()
+        st = self.lib.sm_context_create(device, C.byref(h))
+        if st != 0:
+            raise RuntimeError(f"sm_context_create failed: {STATUS_NAMES.get(st, st)}")
+        self.handle = h
+        self._buffers: list[Buffer] = []
+
+    def register(self, tensor) -> Buffer:
+        if not tensor.is_cuda or not tensor.is_contiguous():
+            raise ValueError("register() needs a contiguous device tensor")
+        hd = C.c_uint64()
+        st = self.lib.sm_buffer_register(self.handle, C.c_void_p(tensor.data_ptr()),
+                                         tensor.numel() * tensor.element_size(), C.byref(hd))
+        if st != 0:
+            raise RuntimeError(f"sm_buffer_register failed: {STATUS_NAMES.get(st, st)}")
+        b = Buffer(self, tensor, hd.value)
+        self._buffers.append(b)
+        return b
+
+    def segment(self) -> "Segment":
+        return Segment(self)
+
+    def read_layer_status(self, stream, plan: View, gate_up_status: View = NULL_VIEW,
+                          down_status: View = NULL_VIEW):
+        bad, gu, dn = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        st = self.lib.sm_read_layer_status(self.handle, C.c_void_p(stream), plan, gate_up_status,
+                                           down_status, C.byref(bad), C.byref(gu), C.byref(dn))
+        if st != 0:
+            raise RuntimeError(f"sm_read_layer_status failed: {STATUS_NAMES.get(st, st)}")
+        return bad.value, gu.value, dn.value
+
+    def close(self):
+        if self.handle:
+            self.lib.sm_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ExpertTable:
+    """Host copy of the [E][3] (gate, up, down) expert address table plus its storage."""
+
+    def __init__(self, addresses: Sequence[int], snapshot: View, storage: Sequence[View]):
+        n = len(addresses)
+        self._addr = (C.c_uint64 * n)(*addresses)
+        self._storage = (View * max(1, len(storage)))(*storage)
+        self.struct = ExpertWeights(C.cast(self._addr, C.POINTER(C.c_uint64)), snapshot,
+                                    C.cast(self._storage, C.POINTER(View)), len(storage))
+
+
+class Segment:
+    """An ordered, validated list of launches: commit() runs it, abort() discards it."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        h = C.c_void_p()
+        st = self.lib.sm_segment_begin(ctx.handle, C.byref(h))
+        if st != 0:
+            raise RuntimeError("sm_segment_begin failed")
+        self.handle = h
+        self._keep: list = []
+
+    def _ret(self, st: int):
+        if st == 0:
+            return True, ""
+        return False, self.error() or STATUS_NAMES.get(st, str(st))
+
+    def error(self) -> str:
+        msg = self.lib.sm_segment_error(self.handle)
+        return msg.decode() if msg else ""
+
+    @property
+    def launches(self) -> int:
+        return int(self.lib.sm_segment_launches(self.handle))
+
+    # Reference coordinator names (namespace strata::metal):
+    def encode_moe_route(self, shape: Shape, divide_weights: bool, b: RouteBuffers):
+        return self._ret(self.lib.sm_encode_route(self.handle, C.byref(shape), int(divide_weights), C.byref(b)))
+
+    def encode_prefill_moe_grouping(self, shape: Shape, b: GroupingBuffers):
+        return self._ret(self.lib.sm_encode_grouping(self.handle, C.byref(shape), C.byref(b)))
+
+    def encode_prefill_moe_full_mode_route_gather(self, shape: Shape, b: RouteGatherBuffers):
+        return self._ret(self.lib.sm_encode_route_gather(self.handle, C.byref(shape), C.byref(b)))
+
+    def encode_prefill_moe_shared_ffn(self, shape: Shape, fmt: int, b: SharedBuffers):
+        return self._ret(self.lib.sm_encode_shared_ffn(self.handle, C.byref(shape), fmt, C.byref(b)))
+
+    def encode_prefill_moe_gu(self, shape: Shape, fmt: int, b: GateUpBuffers, keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_gate_up(self.handle, C.byref(shape), fmt, C.byref(b)))
+
+    def encode_prefill_moe_down(self, shape: Shape, fmt: int, b: DownBuffers, keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_down(self.handle, C.byref(shape), fmt, C.byref(b)))
+
+    def encode_prefill_moe_swiglu(self, rows: int, width: int, b: SwiGLUBuffers):
+        return self._ret(self.lib.sm_encode_swiglu(self.handle, rows, width, C.byref(b)))
+
+    def encode_prefill_moe_combine(self, shape: Shape, b: CombineBuffers):
+        return self._ret(self.lib.sm_encode_combine(self.handle, C.byref(shape), C.byref(b)))
+
+    def encode_prefill_moe_full_mode_layer(self, shape: Shape, formats: LayerFormats,
+                                           b: LayerBuffers, keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_full_layer(self.handle, C.byref(shape), C.byref(formats),
+                                                       C.byref(b)))
+
+    def commit(self, stream=0) -> None:
+        st = self.lib.sm_segment_commit(self.handle, C.c_void_p(stream))
+        self.handle = None
+        if st != 0:
+            raise RuntimeError(f"sm_segment_commit failed: {STATUS_NAMES.get(st, st)}")
+
+    def abort(self) -> None:
+        if self.handle:
+            self.lib.sm_segment_abort(self.handle)
+            self.handle = None
+
+
+# ---- synthetic inputs (host numpy arrays) ------------------------------------------------
+
+def synth_normal_f32(seed: int, stream: int, sigma: float, n: int):
+    import numpy as np
+    out = np.empty(n, np.float32)
+    library().sm_synth_normal_f32(seed, stream, sigma, out.ctypes.data, n)
+    return out
+
+
+def synth_normal_f16(seed: int, stream: int, sigma: float, n: int):
+    import numpy as np
+    out = np.empty(n, np.uint16)
+    library().sm_synth_normal_f16(seed, stream, sigma, out.ctypes.data, n)
+    return out
+
+
+def synth_normal_bf16(seed: int, stream: int, sigma: float, n: int):
+    import numpy as np
+    out = np.empty(n, np.uint16)
+    library().sm_synth_normal_bf16(seed, stream, sigma, out.ctypes.data, n)
+    return out
+
+
+def quantize(fmt: int, x, rows: int, k: int):
+    import numpy as np
+    out = np.empty(rows * row_bytes(fmt, k), np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    st = library().sm_quantize(fmt, x.ctypes.data, rows, k, out.ctypes.data)
+    if st != 0:
+        raise RuntimeError(f"sm_quantize failed: {STATUS_NAMES.get(st, st)}")
+    return out
+
+
+def synth_quantized(fmt: int, seed: int, stream: int, sigma: float, rows: int, k: int):
+    import numpy as np
+    out = np.empty(rows * row_bytes(fmt, k), np.uint8)
+    st = library().sm_synth_quantized(fmt, seed, stream, sigma, rows, k, out.ctypes.data)
+    if st != 0:
+        raise RuntimeError(f"sm_synth_quantized failed: {STATUS_NAMES.get(st, st)}")
+    return out
