@@ -30,6 +30,20 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def calibrate_copy() -> int:
+    """A plain device-to-device copy of 512 MiB, 5 times: the reference point that scales
+    the FETCH_SIZE / WRITE_SIZE counters (each launch moves 512 MiB in and 512 MiB out)."""
+    import torch
+    n = 512 * 1024 * 1024 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 5}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -38,7 +52,11 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, help="configuration index (0-4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 512 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
               f"multi-GPU path — run with --gpus 1", file=sys.stderr)

@@ -258,6 +258,11 @@ sm_status sm_encode_swiglu(sm_segment* seg, uint32_t rows, uint32_t width,
 /* encode_prefill_moe_combine — prefill_moe_post.hpp:46-49. */
 sm_status sm_encode_combine(sm_segment* seg, const sm_moe_shape* shape,
                             const sm_combine_buffers* b);
+/* encode_prefill_dequant_<fmt> — prefill_dequant_dispatch.hpp:13-26: expands n_out
+ * row-major weight rows of k values (`weights`) to K-major F16 [k][n_out] (`k_major_f16`),
+ * with the same per-value decoders the expert products use. */
+sm_status sm_encode_dequant(sm_segment* seg, sm_format fmt, uint32_t n_out, uint32_t k, sm_view weights,
+                            sm_view k_major_f16);
 /* encode_prefill_moe_full_mode_layer — prefill_moe_full_pipeline.hpp:68-73. */
 sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b);
@@ -279,6 +284,8 @@ sm_status sm_submit_swiglu(sm_context* ctx, void* stream, uint32_t rows, uint32_
                            const sm_swiglu_buffers* b, char* err, size_t cap);
 sm_status sm_submit_combine(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                             const sm_combine_buffers* b, char* err, size_t cap);
+sm_status sm_submit_dequant(sm_context* ctx, void* stream, sm_format fmt, uint32_t n_out, uint32_t k,
+                            sm_view weights, sm_view k_major_f16, char* err, size_t cap);
 sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b,
                                char* err, size_t cap);

@@ -11,6 +11,14 @@
 namespace sm {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+// Loads through address-space-1 pointers compile to global_load (vmcnt only). Weight
+// pointers read from the expert address table would otherwise be generic (flat) pointers,
+// whose loads also count against lgkmcnt and are then waited on by every LDS barrier.
+template <class T>
+__device__ __forceinline__ T ld_global(const void* p) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) T*>(reinterpret_cast<uintptr_t>(p));
+}
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -54,20 +62,36 @@ __device__ __forceinline__ _Float16 half_sat(float x) {
 // Byte j (0..3) of a dword as an exact float (selected as v_cvt_f32_ubyte{j}).
 __device__ __forceinline__ float ubyte(uint32_t w, int j) { return float((w >> (8 * j)) & 0xffu); }
 
-// Eight values fma(scale, byte_j, bias) from the four bytes of two dwords, rounded once
-// to F16. With every byte < 2^8 and scale carrying <= 17 significant bits the product is
-// exact, so this equals the reference's `scale * q - bias` rounded to F32 then to F16.
+// Keeps a masked dword opaque to the backend so it does not narrow the mask into per-value
+// bit-field extracts; each byte then converts with one v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ uint32_t keep_u32(uint32_t v) {
+    __asm__("" : "+v"(v));
+    return v;
+}
+
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Two F32 values rounded to nearest-even F16 as one packed pair (v_cvt_pk_f16_f32).
+__device__ __forceinline__ half2v cvt_pk_f16(float a, float b) {
+    return __builtin_convertvector(float2v{a, b}, half2v);
+}
+
+// Eight values fma(scale, byte_j, bias) from the four bytes of two dwords, rounded to F32
+// and then to F16 in pairs (v_fma_f32, then v_cvt_pk_f16_f32: two separate roundings). With every byte < 2^8 and scale carrying <= 17 significant bits the
+// product is exact, so this equals the reference's `scale * q - bias` in F32, then F16.
 __device__ __forceinline__ half8 decode8(uint32_t w0, uint32_t w1, float scale, float bias) {
-    half8 h;
-    h[0] = _Float16(__builtin_fmaf(scale, ubyte(w0, 0), bias));
-    h[1] = _Float16(__builtin_fmaf(scale, ubyte(w0, 1), bias));
-    h[2] = _Float16(__builtin_fmaf(scale, ubyte(w0, 2), bias));
-    h[3] = _Float16(__builtin_fmaf(scale, ubyte(w0, 3), bias));
-    h[4] = _Float16(__builtin_fmaf(scale, ubyte(w1, 0), bias));
-    h[5] = _Float16(__builtin_fmaf(scale, ubyte(w1, 1), bias));
-    h[6] = _Float16(__builtin_fmaf(scale, ubyte(w1, 2), bias));
-    h[7] = _Float16(__builtin_fmaf(scale, ubyte(w1, 3), bias));
-    return h;
+    w0 = keep_u32(w0);
+    w1 = keep_u32(w1);
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[j] = __builtin_fmaf(scale, ubyte(w0, j), bias);
+        f[4 + j] = __builtin_fmaf(scale, ubyte(w1, j), bias);
+    }
+    const half2v p0 = cvt_pk_f16(f[0], f[1]), p1 = cvt_pk_f16(f[2], f[3]);
+    const half2v p2 = cvt_pk_f16(f[4], f[5]), p3 = cvt_pk_f16(f[6], f[7]);
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -81,63 +105,75 @@ __device__ __forceinline__ half8 decode8(uint32_t w0, uint32_t w1, float scale, 
 // Values 64g..64g+31 are the low nibbles of q[32g..32g+31] with pair 2g; values
 // 64g+32..64g+63 the high nibbles with pair 2g+1 (dequant.hpp:157-190).
 struct FragQ4K {
-    uint32_t q[8];
+    u32x4 hdr, qa, qb;
     float d_lo, m_lo, d_hi, m_hi;
-    __device__ __forceinline__ void load(const uint8_t* sb, int g) {
-        const u32x4 hdr = *reinterpret_cast<const u32x4*>(sb);
-        const u32x4 a = *reinterpret_cast<const u32x4*>(sb + 16 + 32 * g);
-        const u32x4 b = *reinterpret_cast<const u32x4*>(sb + 32 + 32 * g);
-        q[0] = a[0]; q[1] = a[1]; q[2] = a[2]; q[3] = a[3];
-        q[4] = b[0]; q[5] = b[1]; q[6] = b[2]; q[7] = b[3];
+    int g;
+    __device__ __forceinline__ void load(const uint8_t* sb, int grp) {
+        g = grp;
+        hdr = ld_global<u32x4>(sb);
+        qa = ld_global<u32x4>(sb + 16 + 32 * grp);
+        qb = ld_global<u32x4>(sb + 32 + 32 * grp);
+    }
+    __device__ __forceinline__ void prepare() {
         const float d = f16_lo(hdr[0]);
         const float dmin = f16_hi(hdr[0]);
-        // scales[12] = bytes 4..15 of the block = hdr[1..3].
-        const uint32_t s0 = hdr[1], s1 = hdr[2], s2 = hdr[3];
-        auto byte = [&](int i) -> uint32_t {
-            const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-            return (w >> (8 * (i & 3))) & 0xffu;
-        };
-        uint32_t sc_lo, mn_lo, sc_hi, mn_hi;
-        const int j0 = 2 * g, j1 = 2 * g + 1;
-        if (j0 < 4) {
-            sc_lo = byte(j0) & 63u; mn_lo = byte(j0 + 4) & 63u;
-            sc_hi = byte(j1) & 63u; mn_hi = byte(j1 + 4) & 63u;
-        } else {
-            sc_lo = (byte(j0 + 4) & 0xFu) | ((byte(j0 - 4) >> 6) << 4);
-            mn_lo = (byte(j0 + 4) >> 4) | ((byte(j0) >> 6) << 4);
-            sc_hi = (byte(j1 + 4) & 0xFu) | ((byte(j1 - 4) >> 6) << 4);
-            mn_hi = (byte(j1 + 4) >> 4) | ((byte(j1) >> 6) << 4);
-        }
+        // scales[12] = bytes 4..15 of the block = hdr[1..3]. Pair j < 4: scale = b[j] & 63,
+        // min = b[j+4] & 63; pair j >= 4: scale = (b[j+4] & 15) | (b[j-4] >> 6) << 4,
+        // min = (b[j+4] >> 4) | (b[j] >> 6) << 4. Lane group g uses pairs 2g, 2g+1; both
+        // forms are computed and selected, so the unpacking has no divergent branch.
+        const uint32_t lo4 = hdr[1], mid4 = hdr[2], hi4 = hdr[3];  // bytes 0-3, 4-7, 8-11
+        const int sh0 = 16 * (g & 1), sh1 = sh0 + 8;                // byte (2g mod 4), +1
+        const uint32_t a0 = (lo4 >> sh0) & 0xffu, a1 = (lo4 >> sh1) & 0xffu;   // b[j], j in 0..3
+        const uint32_t m0 = (mid4 >> sh0) & 0xffu, m1 = (mid4 >> sh1) & 0xffu; // b[j+4]
+        const uint32_t h0 = (hi4 >> sh0) & 0xffu, h1 = (hi4 >> sh1) & 0xffu;   // b[j+8]
+        const bool low = g < 2;
+        const uint32_t sc_lo = low ? (a0 & 63u) : ((h0 & 0xFu) | ((a0 >> 6) << 4));
+        const uint32_t mn_lo = low ? (m0 & 63u) : ((h0 >> 4) | ((m0 >> 6) << 4));
+        const uint32_t sc_hi = low ? (a1 & 63u) : ((h1 & 0xFu) | ((a1 >> 6) << 4));
+        const uint32_t mn_hi = low ? (m1 & 63u) : ((h1 >> 4) | ((m1 >> 6) << 4));
         d_lo = d * float(sc_lo); m_lo = -(dmin * float(mn_lo));
         d_hi = d * float(sc_hi); m_hi = -(dmin * float(mn_hi));
     }
+    __device__ __forceinline__ uint32_t q(int i) const { return i < 4 ? qa[i] : qb[i - 4]; }
     __device__ __forceinline__ half8 step(int s) const {
-        if (s < 4) return decode8(q[2 * s] & 0x0F0F0F0Fu, q[2 * s + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
-        return decode8((q[2 * s - 8] >> 4) & 0x0F0F0F0Fu, (q[2 * s - 7] >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
+        if (s < 4) return decode8(q(2 * s) & 0x0F0F0F0Fu, q(2 * s + 1) & 0x0F0F0F0Fu, d_lo, m_lo);
+        return decode8((q(2 * s - 8) >> 4) & 0x0F0F0F0Fu, (q(2 * s - 7) >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
     }
 };
 
 // Q8_0 (34 B / 32): f16 d, int8 q[32]. A 256-value slab is 8 blocks (272 B); group g owns
-// blocks 2g and 2g+1 (68 B at a 4-byte-aligned offset). Bytes are biased by 128 so the
-// unsigned byte converters apply: d*(u - 128) = fma(d, u, -128 d), exact (dequant.hpp:81-86).
+// blocks 2g and 2g+1 (68 B at a 4-byte-aligned offset). The value is d*q rounded to F16
+// (dequant.hpp:81-86); d*q is exact in F32 (11 x 8 bits), so one F16 rounding of the exact
+// product is the same value. Decoding runs on packed F16 pairs: the byte, biased by 128, is
+// placed under the exponent of 1024 (0x6400 | u = 1024 + u exactly), 1152 is subtracted
+// (exact, giving q), and v_pk_mul_f16 rounds q*d once. A zero code keeps the sign of d.
+__device__ __forceinline__ half2v q80_pair(uint32_t u, uint32_t sel, half2v dd) {
+    const uint32_t biased = __builtin_amdgcn_perm(0u, u, sel) | 0x64006400u;
+    const half2v q = __builtin_bit_cast(half2v, biased) + half2v{_Float16(-1152.0f), _Float16(-1152.0f)};
+    return q * dd;
+}
 struct FragQ80 {
     uint32_t w[17];
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(slab + 68 * g);
+        const uint8_t* p = slab + 68 * g;
 #pragma unroll
-        for (int i = 0; i < 17; ++i) w[i] = p[i];
+        for (int i = 0; i < 17; ++i) w[i] = ld_global<uint32_t>(p + 4 * i);
     }
+    __device__ __forceinline__ void prepare() {}
     // Block b (0/1) occupies bytes 34b .. 34b+33 of the 68: d at 34b, q at 34b+2.
     __device__ __forceinline__ half8 step(int s) const {
         const int b = s >> 2;          // block
         const int o = 34 * b + 2 + 8 * (s & 3);  // byte offset of the 8 quants
         const int wi = o >> 2;
         const int sh = (o & 3) * 8;    // 0 or 16
-        const uint32_t x0 = sh ? __builtin_amdgcn_alignbyte(w[wi + 1], w[wi], 2) : w[wi];
-        const uint32_t x1 = sh ? __builtin_amdgcn_alignbyte(w[wi + 2], w[wi + 1], 2) : w[wi + 1];
+        const uint32_t x0 = (sh ? __builtin_amdgcn_alignbyte(w[wi + 1], w[wi], 2) : w[wi]) ^ 0x80808080u;
+        const uint32_t x1 = (sh ? __builtin_amdgcn_alignbyte(w[wi + 2], w[wi + 1], 2) : w[wi + 1]) ^ 0x80808080u;
         const uint32_t dw = w[(34 * b) >> 2];
-        const float d = b == 0 ? f16_lo(dw) : f16_hi(dw);
-        return decode8(x0 ^ 0x80808080u, x1 ^ 0x80808080u, d, -128.0f * d);
+        const _Float16 d = bits_f16(uint16_t(b == 0 ? (dw & 0xffffu) : (dw >> 16)));
+        const half2v dd{d, d};
+        const half2v p0 = q80_pair(x0, 0x0c010c00u, dd), p1 = q80_pair(x0, 0x0c030c02u, dd);
+        const half2v p2 = q80_pair(x1, 0x0c010c00u, dd), p3 = q80_pair(x1, 0x0c030c02u, dd);
+        return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
     }
 };
 
@@ -146,22 +182,23 @@ struct FragQ80 {
 // q[32n + w] and scale byte 8n + 2j + (w >= 16) (ggml's dequantize_row_q2_K). Group g
 // owns n = g/2, j in {2(g%2), 2(g%2)+1}.
 struct FragQ2K {
-    uint32_t q[8];
-    uint32_t sc;
+    u32x4 qa, qb;
+    uint32_t sc, dd;
     float d, dmin;
     int jbase;
     __device__ __forceinline__ void load(const uint8_t* sb, int g) {
         const int n = g >> 1;
         jbase = 2 * (g & 1);
-        const u32x4 a = *reinterpret_cast<const u32x4*>(sb + 16 + 32 * n);
-        const u32x4 b = *reinterpret_cast<const u32x4*>(sb + 32 + 32 * n);
-        q[0] = a[0]; q[1] = a[1]; q[2] = a[2]; q[3] = a[3];
-        q[4] = b[0]; q[5] = b[1]; q[6] = b[2]; q[7] = b[3];
-        sc = *reinterpret_cast<const uint32_t*>(sb + 8 * n + 2 * jbase);
-        const uint32_t dd = *reinterpret_cast<const uint32_t*>(sb + 80);
+        qa = ld_global<u32x4>(sb + 16 + 32 * n);
+        qb = ld_global<u32x4>(sb + 32 + 32 * n);
+        sc = ld_global<uint32_t>(sb + 8 * n + 2 * jbase);
+        dd = ld_global<uint32_t>(sb + 80);
+    }
+    __device__ __forceinline__ void prepare() {
         d = f16_lo(dd);
         dmin = f16_hi(dd);
     }
+    __device__ __forceinline__ uint32_t q(int i) const { return i < 4 ? qa[i] : qb[i - 4]; }
     __device__ __forceinline__ half8 step(int s) const {
         const int jj = s >> 2;                 // 0/1 -> plane j = jbase + jj
         const int w0 = 8 * (s & 3);            // first w of the 8
@@ -169,8 +206,8 @@ struct FragQ2K {
         const uint32_t scb = (sc >> (8 * (2 * jj + (w0 >= 16 ? 1 : 0)))) & 0xffu;
         const float dl = d * float(scb & 0xFu);
         const float ml = -(dmin * float(scb >> 4));
-        const uint32_t x0 = (q[w0 >> 2] >> shift) & 0x03030303u;
-        const uint32_t x1 = (q[(w0 >> 2) + 1] >> shift) & 0x03030303u;
+        const uint32_t x0 = (q(w0 >> 2) >> shift) & 0x03030303u;
+        const uint32_t x1 = (q((w0 >> 2) + 1) >> shift) & 0x03030303u;
         return decode8(x0, x1, dl, ml);
     }
 };
@@ -179,10 +216,10 @@ struct FragQ2K {
 struct FragF16 {
     half8 v[8];
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
-        const half8* p = reinterpret_cast<const half8*>(slab + 128 * g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = p[i];
+        for (int i = 0; i < 8; ++i) v[i] = ld_global<half8>(slab + 128 * g + 16 * i);
     }
+    __device__ __forceinline__ void prepare() {}
     __device__ __forceinline__ half8 step(int s) const { return v[s]; }
 };
 
@@ -190,10 +227,10 @@ struct FragF16 {
 struct FragBF16 {
     u32x4 v[8];
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(slab + 128 * g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = p[i];
+        for (int i = 0; i < 8; ++i) v[i] = ld_global<u32x4>(slab + 128 * g + 16 * i);
     }
+    __device__ __forceinline__ void prepare() {}
     __device__ __forceinline__ half8 step(int s) const {
         half8 h;
 #pragma unroll

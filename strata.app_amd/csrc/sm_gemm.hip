@@ -23,46 +23,73 @@ constexpr int kLdsRow = kSlab + 8;  // halves
 
 enum Mode { kGateUp = 0, kDown = 1 };
 
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t nb) {
-    // Hardware dispatches workgroup b to XCD b % 8; give each XCD a contiguous run of items.
-    const uint32_t per = nb >> 3;
-    return (b & 7u) * per + (b >> 3);
+// Hardware dispatches workgroup b to XCD b % 8. Give each XCD a contiguous run of the
+// `real` work items (so the column tiles of one row tile share an XCD's L2), spread over
+// all eight XCDs; returns `real` (no work) for blocks past the last item.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t real) {
+    const uint32_t per = (real + 7u) >> 3;
+    const uint32_t slot = b >> 3;
+    if (slot >= per) return real;
+    const uint32_t w = (b & 7u) * per + slot;
+    return w < real ? w : real;
 }
 
-template <class Frag>
+// One 64-row x 128-column tile over all K. Software-pipelined: while slab sb is decoded
+// and multiplied, the raw weight fragments and the activation chunk of slab sb+1 are
+// already in flight into registers; one LDS buffer holds the current activation slab.
+// FULL: K is a multiple of 256, so every load is unconditional and the loop has no
+// divergent branches; otherwise (Q8_0 widths that end mid-slab) lane groups past K load
+// from a clamped in-bounds address and contribute zero weights and activations.
+template <class Frag, bool FULL>
 __device__ __forceinline__ void tile_mma(const _Float16* __restrict__ a_rows, uint32_t a0,
-                                         uint32_t a_last, uint32_t K, const uint8_t* w0row,
+                                         uint32_t a_last, uint32_t K, uint32_t n_rb, const uint8_t* w0row,
                                          const uint8_t* w1row, _Float16* sa, float4v (&acc0)[4],
                                          float4v (&acc1)[4]) {
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
     constexpr int kSB = SlabBytes<Frag>::value;
     const uint32_t n_slabs = (K + kSlab - 1) / kSlab;
-    for (uint32_t sb = 0; sb < n_slabs; ++sb) {
-        const uint32_t k0 = sb * kSlab;
-        const bool kok = k0 + 64u * g < K;
-        Frag f0, f1;
-        if (kok) {
-            f0.load(w0row + uint64_t(sb) * kSB, g);
-            f1.load(w1row + uint64_t(sb) * kSB, g);
+    // Activation staging: thread covers rows r0 + 8i (i = 0..7), 16-byte column cc.
+    const int cc = tid & 31, r0 = tid >> 5;
+    const _Float16* arow[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t row = a0 + r0 + 8 * i;
+        if (row > a_last) row = a_last;
+        arow[i] = a_rows + uint64_t(row) * K + 8 * cc;
+    }
+    const half8 zero{0, 0, 0, 0, 0, 0, 0, 0};
+    half8 areg[8];
+    Frag f0, f1;
+    auto load_slab = [&](uint32_t sb) {
+        uint32_t ka = sb * kSlab, kb = sb;
+        if (!FULL) {
+            if (ka + 8u * cc >= K) ka = 0;             // clamped; zeroed below
+            if (sb * kSlab + 64u * g >= K) kb = 0;     // clamped; zeroed at decode time
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c >> 5, cc = c & 31;
-            uint32_t row = a0 + r;
-            if (row > a_last) row = a_last;
-            const uint32_t kk = k0 + 8 * cc;
-            half8 v;
-            if (kk < K) v = *reinterpret_cast<const half8*>(a_rows + uint64_t(row) * K + kk);
-            else v = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            *reinterpret_cast<half8*>(sa + r * kLdsRow + 8 * cc) = v;
+        for (int i = 0; i < 8; ++i) areg[i] = *reinterpret_cast<const half8*>(arow[i] + ka);
+        if (!FULL && sb * kSlab + 8u * cc >= K) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) areg[i] = zero;
         }
+        f0.load(w0row + uint64_t(kb) * kSB, g);
+        f1.load(w1row + uint64_t(kb) * kSB, g);
+    };
+    load_slab(0);
+    for (uint32_t sb = 0; sb < n_slabs; ++sb) {
+        __syncthreads();  // every wave is done reading the previous slab
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<half8*>(sa + (r0 + 8 * i) * kLdsRow + 8 * cc) = areg[i];
+        Frag c0 = f0, c1 = f1;
+        const bool kok = FULL || sb * kSlab + 64u * g < K;
+        if (sb + 1 < n_slabs) load_slab(sb + 1);
         __syncthreads();
+        c0.prepare();
+        c1.prepare();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const half8 zero{0, 0, 0, 0, 0, 0, 0, 0};
-            const half8 b0 = kok ? f0.step(s) : zero;
-            const half8 b1 = kok ? f1.step(s) : zero;
+            half8 b0 = c0.step(s), b1 = c1.step(s);
+            if (!FULL && !kok) { b0 = zero; b1 = zero; }
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
                 const half8 a = *reinterpret_cast<const half8*>(sa + (16 * rb + n) * kLdsRow + 64 * g + 8 * s);
@@ -70,7 +97,27 @@ __device__ __forceinline__ void tile_mma(const _Float16* __restrict__ a_rows, ui
                 acc1[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc1[rb], 0, 0, 0);
             }
         }
-        __syncthreads();
+    }
+}
+
+// Dequantize rows x K weights of one format to K-major F16 [K][rows] through the same
+// per-lane fragments the products use (one wave per 16 rows x one 256-value slab).
+template <class Frag>
+__global__ __launch_bounds__(64) void decode_rows_kernel(const uint8_t* __restrict__ w, uint32_t rows,
+                                                         uint32_t K, uint64_t row_bytes,
+                                                         uint16_t* __restrict__ out) {
+    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+    const uint32_t row = blockIdx.x * 16u + n, sb = blockIdx.y;
+    constexpr int kSB = SlabBytes<Frag>::value;
+    if (row >= rows || sb * kSlab + 64u * g >= K) return;
+    Frag f;
+    f.load(w + uint64_t(row) * row_bytes + uint64_t(sb) * kSB, g);
+    f.prepare();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const half8 h = f.step(s);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[uint64_t(sb * kSlab + 64u * g + 8u * s + i) * rows + row] = f16_bits(h[i]);
     }
 }
 
@@ -91,22 +138,28 @@ __device__ void zero_tile(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_
     }
 }
 
-template <class Frag, int MODE>
+template <class Frag, int MODE, bool FULL>
 __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t n_ntiles, uint32_t total) {
     __shared__ __attribute__((aligned(16))) _Float16 sa[kRows * kLdsRow];
-    __shared__ uint32_t s_flag;
-    const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
-    if (w >= total) return;
-    const uint32_t tile_index = w / n_ntiles, nt = w % n_ntiles;
+    __shared__ uint32_t s_flag, s_tiles;
     const Plan* p = g.plan;
     const uint32_t N = g.n_entries;
-    if (threadIdx.x == 0) s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+        s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_tiles = p->n_tiles;
+    }
     __syncthreads();
     if (s_flag & 2u) {  // invalid plan or permutation: every tile slot writes zeros
+        if (blockIdx.x >= total) return;
+        const uint32_t tile_index = blockIdx.x / n_ntiles, nt = blockIdx.x % n_ntiles;
         zero_tile<MODE>(g, tile_index * 64u, tile_index * 64u + 64u, nt);
         return;
     }
-    if (tile_index >= p->n_tiles) return;
+    // A valid plan has n_tiles <= capacity; only those tiles carry work.
+    const uint32_t real = (s_tiles < g.tile_capacity ? s_tiles : g.tile_capacity) * n_ntiles;
+    const uint32_t w = xcd_remap(blockIdx.x, real);
+    if (w >= real) return;
+    const uint32_t tile_index = w / n_ntiles, nt = w % n_ntiles;
     const uint32_t tg = g.tiles[2 * tile_index], a0 = g.tiles[2 * tile_index + 1];
     bool ok = tg < p->n_groups;
     uint32_t gfirst = 0, gend = 0;
@@ -152,8 +205,8 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
     float4v acc0[4], acc1[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
-    tile_mma<Frag>(g.a, a0, a1 - 1u, g.k, w0 + uint64_t(col0) * g.row_bytes, w1 + uint64_t(col1) * g.row_bytes,
-                   sa, acc0, acc1);
+    tile_mma<Frag, FULL>(g.a, a0, a1 - 1u, g.k, (a1 - a0 + 15u) / 16u, w0 + uint64_t(col0) * g.row_bytes,
+                   w1 + uint64_t(col1) * g.row_bytes, sa, acc0, acc1);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -180,7 +233,7 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
 template <class Frag, int MODE>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseGemm g, uint32_t n_ntiles, uint32_t total) {
     __shared__ __attribute__((aligned(16))) _Float16 sa[kRows * kLdsRow];
-    const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t w = xcd_remap(blockIdx.x, total);
     if (w >= total) return;
     const uint32_t mt = w / n_ntiles, nt = w % n_ntiles;
     const uint32_t r0 = mt * 64u;
@@ -196,8 +249,8 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseGemm g, uint32_t n
     float4v acc0[4], acc1[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
-    tile_mma<Frag>(g.a, r0, r1 - 1u, g.k, w0 + uint64_t(col0) * g.row_bytes, w1 + uint64_t(col1) * g.row_bytes,
-                   sa, acc0, acc1);
+    tile_mma<Frag, true>(g.a, r0, r1 - 1u, g.k, (r1 - r0 + 15u) / 16u, w0 + uint64_t(col0) * g.row_bytes,
+                   w1 + uint64_t(col1) * g.row_bytes, sa, acc0, acc1);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -238,7 +291,8 @@ hipError_t launch_routed(const RoutedGemm& g, hipStream_t s) {
     const uint32_t n_ntiles = MODE == kGateUp ? g.n_out / 64u : g.n_out / 128u;
     const uint32_t total = g.tile_capacity * n_ntiles;
     const uint32_t blocks = (total + 7u) & ~7u;
-    routed_gemm_kernel<Frag, MODE><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
+    if (g.k % kSlab == 0) routed_gemm_kernel<Frag, MODE, true><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
+    else routed_gemm_kernel<Frag, MODE, false><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
     return hipGetLastError();
 }
 
@@ -285,6 +339,19 @@ hipError_t launch_dense_down(Fmt fmt, const DenseGemm& g, hipStream_t s) {
         case Fmt::BF16: return launch_dense<FragBF16, kDown>(g, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_decode_rows(Fmt fmt, const uint8_t* w, uint32_t rows, uint32_t k, uint64_t row_bytes,
+                              uint16_t* out, hipStream_t s) {
+    const dim3 grid((rows + 15u) / 16u, (k + kSlab - 1) / kSlab);
+    switch (fmt) {
+        case Fmt::Q8_0: decode_rows_kernel<FragQ80><<<grid, 64, 0, s>>>(w, rows, k, row_bytes, out); break;
+        case Fmt::Q4_K: decode_rows_kernel<FragQ4K><<<grid, 64, 0, s>>>(w, rows, k, row_bytes, out); break;
+        case Fmt::Q2_K: decode_rows_kernel<FragQ2K><<<grid, 64, 0, s>>>(w, rows, k, row_bytes, out); break;
+        case Fmt::F16: decode_rows_kernel<FragF16><<<grid, 64, 0, s>>>(w, rows, k, row_bytes, out); break;
+        case Fmt::BF16: decode_rows_kernel<FragBF16><<<grid, 64, 0, s>>>(w, rows, k, row_bytes, out); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gate_logit(Fmt fmt, const _Float16* x, const uint8_t* gv, float* gl, uint32_t rows,

@@ -79,6 +79,11 @@ hipError_t launch_dense_down(Fmt fmt, const DenseGemm& g, hipStream_t s);
 hipError_t launch_gate_logit(Fmt fmt, const _Float16* x, const uint8_t* gv, float* gl, uint32_t rows,
                              uint32_t d, hipStream_t s);
 
+// Decode `rows` weight rows of `k` values to K-major F16 bits [k][rows], through the
+// products' own per-lane fragment decoders.
+hipError_t launch_decode_rows(Fmt fmt, const uint8_t* w, uint32_t rows, uint32_t k, uint64_t row_bytes,
+                              uint16_t* out, hipStream_t s);
+
 // ---- post ops ----
 hipError_t launch_swiglu(const float* gate, const float* up, _Float16* out, uint64_t n,
                          hipStream_t s);

@@ -353,44 +353,49 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
 // Expert-stage validation (prefill_moe.metal:603-733): status is cleared, then bit 1 set
 // when the plan header, the tile chain, or the destination permutation is inconsistent.
 // ---------------------------------------------------------------------------------------
-__device__ bool plan_header_valid(const Plan* p, uint32_t N, uint32_t E, uint32_t cap) {
-    if (p->bad != 0u || p->n_groups == 0u || p->n_groups > E || p->n_groups > 512u ||
-        p->n_entries != N || p->n_tiles > cap || p->n_tiles > p->n_entries ||
-        p->grp_start[0] != 0 || p->grp_start[p->n_groups] != int32_t(N))
-        return false;
-    uint32_t expected = 0;
-    int32_t prev_end = 0;
-    for (uint32_t g = 0; g < p->n_groups; ++g) {
-        const int32_t first = p->grp_start[g], end = p->grp_start[g + 1], ex = p->grp_e[g];
-        if (first != prev_end || end <= first || uint32_t(end) > N || ex < 0 || uint32_t(ex) >= E)
-            return false;
-        if (g != 0u && ex <= p->grp_e[g - 1]) return false;
-        prev_end = end;
-        const uint32_t c = uint32_t(end - first);
-        expected += (c + kExpertTile - 1) / kExpertTile;
-        if (expected > cap) return false;
-    }
-    return prev_end == int32_t(N) && expected == p->n_tiles;
-}
-
-__global__ __launch_bounds__(256) void plan_validate_kernel(const Plan* __restrict__ p,
+// The header and per-group checks run one group per thread; the tile-count sum is a block
+// reduction, so the whole plan is checked in a few dependent memory round trips.
+__global__ __launch_bounds__(512) void plan_validate_kernel(const Plan* __restrict__ p,
                                                             const uint32_t* __restrict__ tiles,
                                                             uint32_t* __restrict__ status, uint32_t N,
                                                             uint32_t E, uint32_t cap) {
-    __shared__ uint32_t header_ok;
-    const uint32_t tid = threadIdx.x;
+    __shared__ uint32_t s_header_ok, s_groups_ok, s_wave_tiles[8];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t ng = p->n_groups, nt = p->n_tiles;
     if (tid == 0) {
         *status = 0u;
-        header_ok = plan_header_valid(p, N, E, cap) ? 1u : 0u;
+        s_groups_ok = 1u;
+        s_header_ok = (p->bad == 0u && ng != 0u && ng <= E && ng <= 512u && p->n_entries == N && nt <= cap &&
+                       nt <= p->n_entries && p->grp_start[0] == 0 && p->grp_start[ng] == int32_t(N))
+                          ? 1u : 0u;
     }
     __syncthreads();
-    if (!header_ok) {
+    if (!s_header_ok) {
         if (tid == 0) atomicOr(status, 2u);
         return;
     }
-    for (uint32_t i = tid; i < p->n_tiles; i += 256) {
+    // Group g: non-empty, inside [0, N), expert in range and strictly ascending.
+    uint32_t my_tiles = 0;
+    for (uint32_t g = tid; g < ng; g += 512u) {
+        const int32_t first = p->grp_start[g], end = p->grp_start[g + 1], ex = p->grp_e[g];
+        bool ok = end > first && uint32_t(end) <= N && ex >= 0 && uint32_t(ex) < E;
+        if (g != 0u) ok = ok && ex > p->grp_e[g - 1];
+        if (!ok) s_groups_ok = 0u;
+        else my_tiles += (uint32_t(end - first) + kExpertTile - 1) / kExpertTile;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) my_tiles += __shfl_xor(my_tiles, off);
+    if (lane == 0) s_wave_tiles[wave] = my_tiles;
+    __syncthreads();
+    uint32_t expected = 0;
+    for (uint32_t w = 0; w < 8; ++w) expected += s_wave_tiles[w];
+    if (!s_groups_ok || expected != nt) {
+        if (tid == 0) atomicOr(status, 2u);
+        return;
+    }
+    for (uint32_t i = tid; i < nt; i += 512u) {
         const uint32_t tg = tiles[2 * i], ty = tiles[2 * i + 1];
-        bool ok = tg < p->n_groups;
+        bool ok = tg < ng;
         if (ok) {
             const uint32_t first = uint32_t(p->grp_start[tg]), end = uint32_t(p->grp_start[tg + 1]);
             ok = ty >= first && ty < end && (ty - first) % kExpertTile == 0u;
@@ -398,12 +403,12 @@ __global__ __launch_bounds__(256) void plan_validate_kernel(const Plan* __restri
                 ok = ok && tg == 0u && ty == 0u;
             } else {
                 const uint32_t pg = tiles[2 * (i - 1)], py = tiles[2 * (i - 1) + 1];
-                if (pg >= p->n_groups) ok = false;
+                if (pg >= ng) ok = false;
                 else if (pg == tg) ok = ok && ty == py + kExpertTile;
                 else if (pg + 1u == tg) ok = ok && py + kExpertTile >= uint32_t(p->grp_start[pg + 1]) && ty == first;
                 else ok = false;
             }
-            if (i + 1u == p->n_tiles) ok = ok && tg + 1u == p->n_groups && ty + kExpertTile >= end;
+            if (i + 1u == nt) ok = ok && tg + 1u == ng && ty + kExpertTile >= end;
         }
         if (!ok) atomicOr(status, 2u);
     }
@@ -470,7 +475,7 @@ hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int
 
 hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status, uint32_t N,
                                 uint32_t E, uint32_t cap, hipStream_t s) {
-    plan_validate_kernel<<<1, 256, 0, s>>>(plan, tiles, status, N, E, cap);
+    plan_validate_kernel<<<1, 512, 0, s>>>(plan, tiles, status, N, E, cap);
     return hipGetLastError();
 }
 

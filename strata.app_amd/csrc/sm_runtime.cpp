@@ -734,6 +734,29 @@ sm_status sm_encode_combine(sm_segment* seg, const sm_moe_shape* shape, const sm
     return SM_OK;
 }
 
+sm_status sm_encode_dequant(sm_segment* seg, sm_format fmt, uint32_t n_out, uint32_t k, sm_view weights,
+                            sm_view out) {
+    Check c;
+    const char* P = "Prefill dequant";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    if (!routed_fmt(fmt) && !dense_fmt(fmt)) return record_fail(seg, SM_E_FORMAT, std::string(P) + " format is not supported");
+    if (n_out == 0 || !k_ok(fmt, k)) return record_fail(seg, SM_E_SHAPE, std::string(P) + " widths do not fit the format's blocks");
+    uint64_t w_b, o_b;
+    if (!mul_ok({n_out, fmt_row_bytes(fmt, k)}, w_b) || !mul_ok({n_out, k, 2}, o_b))
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " buffer size overflows");
+    uintptr_t w, o;
+    if (!c.view(weights, w_b, weight_align(fmt), "weights", false, w) || !c.view(out, o_b, 2, "K-major F16", true, o) ||
+        !c.aliases())
+        return finish(seg, c);
+    const uint64_t rb = fmt_row_bytes(fmt, k);
+    add_step(seg, "dequant", [=](hipStream_t s) {
+        return sm::launch_decode_rows(Fmt(fmt), reinterpret_cast<const uint8_t*>(w), n_out, k, rb,
+                                      reinterpret_cast<uint16_t*>(o), s);
+    });
+    return SM_OK;
+}
+
 sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
                                const sm_layer_buffers* b) {
     const char* P = "full-mode Prefill MoE";
@@ -839,6 +862,10 @@ sm_status sm_submit_swiglu(sm_context* ctx, void* stream, uint32_t rows, uint32_
 sm_status sm_submit_combine(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                             const sm_combine_buffers* b, char* err, size_t cap) {
     SM_SUBMIT_BODY(sm_encode_combine(seg, shape, b))
+}
+sm_status sm_submit_dequant(sm_context* ctx, void* stream, sm_format fmt, uint32_t n_out, uint32_t k,
+                            sm_view weights, sm_view out, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_dequant(seg, fmt, n_out, k, weights, out))
 }
 sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b, char* err,

@@ -39,7 +39,7 @@ EXPORTS = (
     "sm_segment_launches",
     "sm_encode_route", "sm_encode_grouping", "sm_encode_route_gather", "sm_encode_shared_ffn",
     "sm_encode_gate_up", "sm_encode_down", "sm_encode_swiglu", "sm_encode_combine",
-    "sm_encode_full_layer",
+    "sm_encode_full_layer", "sm_encode_dequant", "sm_submit_dequant",
     "sm_submit_route", "sm_submit_grouping", "sm_submit_route_gather", "sm_submit_shared_ffn",
     "sm_submit_gate_up", "sm_submit_down", "sm_submit_swiglu", "sm_submit_combine",
     "sm_submit_full_layer", "sm_read_layer_status",
@@ -153,6 +153,7 @@ def library() -> C.CDLL:
         "sm_encode_combine": (I, [P, C.POINTER(Shape), C.POINTER(CombineBuffers)]),
         "sm_encode_full_layer": (I, [P, C.POINTER(Shape), C.POINTER(LayerFormats),
                                      C.POINTER(LayerBuffers)]),
+        "sm_encode_dequant": (I, [P, I, U32, U32, View, View]),
         "sm_submit_full_layer": (I, [P, P, C.POINTER(Shape), C.POINTER(LayerFormats),
                                      C.POINTER(LayerBuffers), C.c_char_p, C.c_size_t]),
         "sm_read_layer_status": (I, [P, P, View, View, View, C.POINTER(U32), C.POINTER(U32),
@@ -315,6 +316,9 @@ class Segment:
         self._keep.append(keep)
         return self._ret(self.lib.sm_encode_full_layer(self.handle, C.byref(shape), C.byref(formats),
                                                        C.byref(b)))
+
+    def encode_prefill_dequant(self, fmt: int, n_out: int, k: int, weights: View, k_major_f16: View):
+        return self._ret(self.lib.sm_encode_dequant(self.handle, fmt, n_out, k, weights, k_major_f16))
 
     def commit(self, stream=0) -> None:
         st = self.lib.sm_segment_commit(self.handle, C.c_void_p(stream))
