@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <functional>
@@ -26,8 +27,13 @@ struct sm_context {
     std::mutex mu;
     struct Alloc { uintptr_t ptr; uint64_t bytes; };
     std::map<uint64_t, Alloc> buffers;
-    uint64_t next_handle = 1;
 };
+
+namespace {
+// Handles are unique across every context of the process, so a view from another context
+// never resolves in this one's registry (the reference's "owned by this Context" check).
+std::atomic<uint64_t> g_next_handle{1};
+}  // namespace
 
 struct sm_segment {
     sm_context* ctx = nullptr;
@@ -534,7 +540,7 @@ void sm_context_destroy(sm_context* ctx) { delete ctx; }
 sm_status sm_buffer_register(sm_context* ctx, void* ptr, uint64_t bytes, uint64_t* handle) {
     if (!ctx || !ptr || !handle || bytes == 0) return SM_E_ARGUMENT;
     std::lock_guard<std::mutex> lk(ctx->mu);
-    const uint64_t h = ctx->next_handle++;
+    const uint64_t h = g_next_handle.fetch_add(1);
     ctx->buffers[h] = {reinterpret_cast<uintptr_t>(ptr), bytes};
     *handle = h;
     return SM_OK;

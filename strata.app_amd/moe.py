@@ -199,6 +199,16 @@ class Buffer:
         return View(self.handle, offset, self.nbytes - offset if length is None else length)
 
 
+class RawBuffer:
+    """A registered raw device address range."""
+
+    def __init__(self, ctx: "Context", ptr: int, nbytes: int, handle: int):
+        self.ctx, self.ptr, self.nbytes, self.handle = ctx, ptr, nbytes, handle
+
+    def view(self, offset: int = 0, length: Optional[int] = None) -> View:
+        return View(self.handle, offset, self.nbytes - offset if length is None else length)
+
+
 class Context:
     """Owns the allocation registry that backs the 'owned by this context' checks."""
 
@@ -222,6 +232,18 @@ class Context:
         b = Buffer(self, tensor, hd.value)
         self._buffers.append(b)
         return b
+
+    def register_ptr(self, ptr: int, nbytes: int) -> "RawBuffer":
+        """Registers a raw device address range (no tensor); used by callers that manage
+        their own allocations and by host-only validation tests."""
+        hd = C.c_uint64()
+        st = self.lib.sm_buffer_register(self.handle, C.c_void_p(ptr), nbytes, C.byref(hd))
+        if st != 0:
+            raise RuntimeError(f"sm_buffer_register failed: {STATUS_NAMES.get(st, st)}")
+        return RawBuffer(self, ptr, nbytes, hd.value)
+
+    def unregister(self, handle: int) -> int:
+        return int(self.lib.sm_buffer_unregister(self.handle, handle))
 
     def segment(self) -> "Segment":
         return Segment(self)
