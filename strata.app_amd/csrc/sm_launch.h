@@ -40,8 +40,11 @@ hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int
                          const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
 
 // ---- expert stage validation (the reference's plan/destination validators) ----
+// Also copies `snap_words` u64 of the validated expert-address table from `snap_src` (pinned
+// host memory; may be null) into the device snapshot `snap_dst` before validating.
 hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status,
                                 uint32_t n_entries, uint32_t n_experts, uint32_t tile_capacity,
+                                const uint64_t* snap_src, uint64_t* snap_dst, uint32_t snap_words,
                                 hipStream_t s);
 hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bitset, uint32_t* status,
                                        uint32_t n_entries, hipStream_t s);

@@ -358,9 +358,13 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
 __global__ __launch_bounds__(512) void plan_validate_kernel(const Plan* __restrict__ p,
                                                             const uint32_t* __restrict__ tiles,
                                                             uint32_t* __restrict__ status, uint32_t N,
-                                                            uint32_t E, uint32_t cap) {
+                                                            uint32_t E, uint32_t cap,
+                                                            const uint64_t* snap_src, uint64_t* snap_dst,
+                                                            uint32_t snap_words) {
     __shared__ uint32_t s_header_ok, s_groups_ok, s_wave_tiles[8];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    if (snap_src != nullptr)
+        for (uint32_t i = tid; i < snap_words; i += 512u) snap_dst[i] = snap_src[i];
     const uint32_t ng = p->n_groups, nt = p->n_tiles;
     if (tid == 0) {
         *status = 0u;
@@ -474,8 +478,9 @@ hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int
 }
 
 hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status, uint32_t N,
-                                uint32_t E, uint32_t cap, hipStream_t s) {
-    plan_validate_kernel<<<1, 512, 0, s>>>(plan, tiles, status, N, E, cap);
+                                uint32_t E, uint32_t cap, const uint64_t* snap_src, uint64_t* snap_dst,
+                                uint32_t snap_words, hipStream_t s) {
+    plan_validate_kernel<<<1, 512, 0, s>>>(plan, tiles, status, N, E, cap, snap_src, snap_dst, snap_words);
     return hipGetLastError();
 }
 

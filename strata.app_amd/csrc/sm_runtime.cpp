@@ -27,6 +27,17 @@ struct sm_context {
     std::mutex mu;
     struct Alloc { uintptr_t ptr; uint64_t bytes; };
     std::map<uint64_t, Alloc> buffers;
+    // Pinned host ring for validated expert-address tables. Allocated once at context
+    // creation; a slot is reused only after the event recorded behind the kernel that read
+    // it has completed.
+    static constexpr uint32_t kRingSlots = 64;
+    static constexpr uint32_t kSlotWords = 3 * 512;
+    uint64_t* ring = nullptr;
+    hipEvent_t ring_ev[kRingSlots] = {};
+    bool ring_pending[kRingSlots] = {};
+    bool ring_claimed[kRingSlots] = {};  // filled by an encode whose segment is not committed yet
+    uint32_t ring_next = 0;
+    std::mutex ring_mu;
 };
 
 namespace {
@@ -37,7 +48,8 @@ std::atomic<uint64_t> g_next_handle{1};
 
 struct sm_segment {
     sm_context* ctx = nullptr;
-    struct Step { std::string label; std::function<hipError_t(hipStream_t)> run; };
+    // ring_slot >= 0: the step reads that pinned ring slot; an event is recorded after it.
+    struct Step { std::string label; std::function<hipError_t(hipStream_t)> run; int ring_slot = -1; };
     std::vector<Step> steps;
     bool failed = false;
     std::string error;
@@ -281,9 +293,32 @@ bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, 
     return true;
 }
 
-// Writes the validated table into the device snapshot from kernel arguments (no host
-// staging memory has to outlive the call).
-void encode_snapshot(sm_segment* seg, const WeightsRes& w);
+// Copies a validated table into a pinned ring slot; the plan-validation kernel of the
+// stage copies it on to the device snapshot. Returns the slot (-1 without a device).
+// Returns -2 when every slot belongs to a segment that has not been committed or aborted,
+// -3 when waiting for a slot's previous copy failed.
+int claim_ring_slot(sm_context* ctx, const std::vector<uint64_t>& table) {
+    if (ctx->ring == nullptr) return -1;
+    std::lock_guard<std::mutex> lk(ctx->ring_mu);
+    for (uint32_t tries = 0; tries < sm_context::kRingSlots; ++tries) {
+        const uint32_t slot = ctx->ring_next++ % sm_context::kRingSlots;
+        if (ctx->ring_claimed[slot]) continue;
+        if (ctx->ring_pending[slot]) {
+            if (hipEventSynchronize(ctx->ring_ev[slot]) != hipSuccess) return -3;
+            ctx->ring_pending[slot] = false;
+        }
+        ctx->ring_claimed[slot] = true;
+        std::memcpy(ctx->ring + uint64_t(slot) * sm_context::kSlotWords, table.data(), table.size() * 8);
+        return int(slot);
+    }
+    return -2;
+}
+
+void release_ring_slots(sm_segment* seg) {
+    std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
+    for (const auto& step : seg->steps)
+        if (step.ring_slot >= 0) seg->ctx->ring_claimed[step.ring_slot] = false;
+}
 
 struct GateUpRes { WeightsRes w; uintptr_t xs, plan, tiles, hidden, status; };
 bool check_gate_up(Check& c, const sm_moe_shape& s, int fmt, const sm_gate_up_buffers& b, GateUpRes& r) {
@@ -303,8 +338,13 @@ bool check_gate_up(Check& c, const sm_moe_shape& s, int fmt, const sm_gate_up_bu
            c.view(b.status, 4, 4, "status", true, r.status);
 }
 
-void encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r) {
-    encode_snapshot(seg, r.w);
+sm_status encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r) {
+    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+    if (slot == -2) return SM_E_SEGMENT;
+    if (slot == -3) return SM_E_DEVICE;
+    const uint64_t* snap_src = slot >= 0 ? seg->ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
+    uint64_t* snap_dst = reinterpret_cast<uint64_t*>(r.w.snapshot);
+    const uint32_t words = uint32_t(r.w.table.size());
     const uint32_t N = s.rows * s.top_k;
     const uint32_t cap = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
     sm::RoutedGemm g{};
@@ -322,9 +362,11 @@ void encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, cons
     g.row_bytes = fmt_row_bytes(fmt, s.hidden);
     const uint32_t E = s.n_experts;
     add_step(seg, "gate/up plan validate", [=](hipStream_t st) {
-        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, st);
+        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, snap_src, snap_dst, words, st);
     });
+    seg->steps.back().ring_slot = slot;
     add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fmt), g, st); });
+    return SM_OK;
 }
 
 struct DownRes { WeightsRes w; uintptr_t hidden, plan, tiles, dst, parts, status; };
@@ -346,8 +388,13 @@ bool check_down(Check& c, const sm_moe_shape& s, int fmt, const sm_down_buffers&
            c.view(b.status, 4, 4, "status", true, r.status);
 }
 
-void encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r) {
-    encode_snapshot(seg, r.w);
+sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r) {
+    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+    if (slot == -2) return SM_E_SEGMENT;
+    if (slot == -3) return SM_E_DEVICE;
+    const uint64_t* snap_src = slot >= 0 ? seg->ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
+    uint64_t* snap_dst = reinterpret_cast<uint64_t*>(r.w.snapshot);
+    const uint32_t words = uint32_t(r.w.table.size());
     const uint32_t N = s.rows * s.top_k;
     const uint32_t cap = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
     sm::RoutedGemm g{};
@@ -366,14 +413,16 @@ void encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const D
     g.row_bytes = fmt_row_bytes(fmt, s.expert_ff);
     const uint32_t E = s.n_experts;
     add_step(seg, "down plan validate", [=](hipStream_t st) {
-        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, st);
+        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, snap_src, snap_dst, words, st);
     });
+    seg->steps.back().ring_slot = slot;
     // The destination bitset borrows the head of `parts`, which the down tiles overwrite
     // (the reference's prefill_moe_down_dispatch.mm:470-520 does the same).
     add_step(seg, "down destination validate", [=](hipStream_t st) {
         return sm::launch_destination_validate(g.dst, reinterpret_cast<uint32_t*>(g.out_f), g.status, N, st);
     });
     add_step(seg, "down tiles", [=](hipStream_t st) { return sm::launch_down(Fmt(fmt), g, st); });
+    return SM_OK;
 }
 
 struct SharedRes { uintptr_t x, wg, wu, wd, gv, hidden, out, gl; };
@@ -448,6 +497,14 @@ void encode_combine_launch(sm_segment* seg, const sm_moe_shape& s, const Combine
     });
 }
 
+const char* const kRingFull =
+    "Prefill MoE expert stage: 64 expert stages are encoded but neither committed nor aborted";
+const char* const kRingWait = "Prefill MoE expert stage: waiting for an address-table copy failed";
+
+sm_status ring_fail(sm_segment* seg, sm_status st) {
+    return record_fail(seg, st, st == SM_E_DEVICE ? kRingWait : kRingFull);
+}
+
 sm_status begin_check(sm_segment* seg, const char* prefix, Check& c) {
     if (seg == nullptr) return SM_E_ARGUMENT;
     c.ctx = seg->ctx;
@@ -481,29 +538,6 @@ bool expected_edge(const Range& w, const Range& r) {
 
 }  // namespace
 
-// Snapshot kernel: one launch per 320 table words.
-struct SnapChunk { uint64_t v[320]; };
-__global__ void snapshot_write_kernel(uint64_t* dst, uint32_t count, SnapChunk chunk) {
-    const uint32_t i = threadIdx.x;
-    if (i < count) dst[i] = chunk.v[i];
-}
-
-namespace {
-void encode_snapshot(sm_segment* seg, const WeightsRes& w) {
-    const uint64_t words = w.table.size();
-    for (uint64_t base = 0; base < words; base += 320) {
-        SnapChunk ch{};
-        const uint32_t count = uint32_t(std::min<uint64_t>(320, words - base));
-        std::memcpy(ch.v, w.table.data() + base, count * 8);
-        uint64_t* dst = reinterpret_cast<uint64_t*>(w.snapshot) + base;
-        add_step(seg, "address snapshot", [=](hipStream_t st) {
-            snapshot_write_kernel<<<1, 320, 0, st>>>(dst, count, ch);
-            return hipGetLastError();
-        });
-    }
-}
-}  // namespace
-
 extern "C" {
 
 uint32_t sm_abi_version(void) { return SM_ABI_VERSION; }
@@ -531,11 +565,33 @@ sm_status sm_context_create(int device, sm_context** out) {
     if (!c) return SM_E_DEVICE;
     c->device = device;
     c->has_device = n > 0;
+    if (c->has_device) {
+        bool ok = hipSetDevice(device) == hipSuccess &&
+                  hipHostMalloc(reinterpret_cast<void**>(&c->ring),
+                                sizeof(uint64_t) * sm_context::kSlotWords * sm_context::kRingSlots,
+                                hipHostMallocDefault) == hipSuccess;
+        for (uint32_t i = 0; ok && i < sm_context::kRingSlots; ++i)
+            ok = hipEventCreateWithFlags(&c->ring_ev[i], hipEventDisableTiming) == hipSuccess;
+        if (!ok) {
+            sm_context_destroy(c);
+            return SM_E_DEVICE;
+        }
+    }
     *out = c;
     return SM_OK;
 }
 
-void sm_context_destroy(sm_context* ctx) { delete ctx; }
+void sm_context_destroy(sm_context* ctx) {
+    if (!ctx) return;
+    // Teardown is best effort: a failed wait or release leaves nothing the caller can act on.
+    for (uint32_t i = 0; i < sm_context::kRingSlots; ++i) {
+        if (ctx->ring_ev[i] == nullptr) continue;
+        if (ctx->ring_pending[i]) (void)hipEventSynchronize(ctx->ring_ev[i]);
+        (void)hipEventDestroy(ctx->ring_ev[i]);
+    }
+    if (ctx->ring) (void)hipHostFree(ctx->ring);
+    delete ctx;
+}
 
 sm_status sm_buffer_register(sm_context* ctx, void* ptr, uint64_t bytes, uint64_t* handle) {
     if (!ctx || !ptr || !handle || bytes == 0) return SM_E_ARGUMENT;
@@ -563,18 +619,30 @@ sm_status sm_segment_begin(sm_context* ctx, sm_segment** out) {
 
 sm_status sm_segment_commit(sm_segment* seg, void* stream) {
     if (!seg) return SM_E_ARGUMENT;
-    if (seg->failed) { delete seg; return SM_E_SEGMENT; }
+    if (seg->failed) { release_ring_slots(seg); delete seg; return SM_E_SEGMENT; }
     sm_status st = SM_OK;
     if (!seg->ctx->has_device || hipSetDevice(seg->ctx->device) != hipSuccess) st = SM_E_DEVICE;
     for (auto& step : seg->steps) {
         if (st != SM_OK) break;
         if (step.run(reinterpret_cast<hipStream_t>(stream)) != hipSuccess) st = SM_E_DEVICE;
+        if (step.ring_slot >= 0) {
+            std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
+            if (hipEventRecord(seg->ctx->ring_ev[step.ring_slot], reinterpret_cast<hipStream_t>(stream)) == hipSuccess)
+                seg->ctx->ring_pending[step.ring_slot] = true;
+            else
+                st = SM_E_DEVICE;
+        }
     }
+    release_ring_slots(seg);
     delete seg;
     return st;
 }
 
-void sm_segment_abort(sm_segment* seg) { delete seg; }
+void sm_segment_abort(sm_segment* seg) {
+    if (!seg) return;
+    release_ring_slots(seg);
+    delete seg;
+}
 
 const char* sm_segment_error(const sm_segment* seg) { return seg ? seg->error.c_str() : ""; }
 uint32_t sm_segment_launches(const sm_segment* seg) { return seg ? uint32_t(seg->steps.size()) : 0; }
@@ -685,7 +753,7 @@ sm_status sm_encode_gate_up(sm_segment* seg, const sm_moe_shape* shape, sm_forma
     if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
     GateUpRes r{};
     if (!check_gate_up(c, *shape, fmt, *b, r) || !c.aliases()) return finish(seg, c);
-    encode_gate_up_launch(seg, *shape, fmt, r);
+    if ((st = encode_gate_up_launch(seg, *shape, fmt, r)) != SM_OK) return ring_fail(seg, st);
     return SM_OK;
 }
 
@@ -699,7 +767,7 @@ sm_status sm_encode_down(sm_segment* seg, const sm_moe_shape* shape, sm_format f
     if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
     DownRes r{};
     if (!check_down(c, *shape, fmt, *b, r) || !c.aliases()) return finish(seg, c);
-    encode_down_launch(seg, *shape, fmt, r);
+    if ((st = encode_down_launch(seg, *shape, fmt, r)) != SM_OK) return ring_fail(seg, st);
     return SM_OK;
 }
 
@@ -814,8 +882,8 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
         }
     encode_route_gather_launch(seg, s, rr, ro, gr);
     if (has_shared) encode_shared_launch(seg, s, f->shared, sr);
-    encode_gate_up_launch(seg, s, f->gate_up, gu);
-    encode_down_launch(seg, s, f->down, dn);
+    if ((st = encode_gate_up_launch(seg, s, f->gate_up, gu)) != SM_OK) return ring_fail(seg, st);
+    if ((st = encode_down_launch(seg, s, f->down, dn)) != SM_OK) return ring_fail(seg, st);
     encode_combine_launch(seg, s, co);
     return SM_OK;
 }
