@@ -22,6 +22,19 @@ __device__ __forceinline__ T ld_global(const void* p) {
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Where a fragment is read from: global memory, or a copy staged in LDS (generic pointers
+// into the workgroup's shared arrays, read through address space 3 as ds_read).
+struct FromGlobal {
+    template <class T>
+    __device__ __forceinline__ static T ld(const uint8_t* p) { return ld_global<T>(p); }
+};
+struct FromLds {
+    template <class T>
+    __device__ __forceinline__ static T ld(const uint8_t* p) {
+        return *(const __attribute__((address_space(3))) T*)(p);
+    }
+};
+
 // exp(x): Cody & Waite reduction x = n*ln2 + r with a two-part ln2, a degree-7 Taylor
 // polynomial in r evaluated by Horner with fma, and an exact scale by 2^n (v_ldexp_f32).
 __device__ __forceinline__ float exp_cw(float x) {
@@ -44,6 +57,15 @@ __device__ __forceinline__ float exp_cw(float x) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + exp_cw(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + exp_cw(-x)); }
+
+// silu for the fused product epilogues, whose F32 inputs already carry accumulation-order
+// rounding: exp2 and the reciprocal come from the hardware (v_exp_f32, v_rcp_f32, each
+// within 1 ulp), a few F32 ulps from silu() above before the result is rounded to F16.
+// Limits match silu(): +inf -> +inf, -inf -> NaN, large negative x -> -0.
+__device__ __forceinline__ float silu_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * -1.44269502162933349609375f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 __device__ __forceinline__ uint16_t f16_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ _Float16 bits_f16(uint16_t u) { return __builtin_bit_cast(_Float16, u); }
@@ -108,29 +130,35 @@ struct FragQ4K {
     u32x4 hdr, qa, qb;
     float d_lo, m_lo, d_hi, m_hi;
     int g;
+    template <class M = FromGlobal>
     __device__ __forceinline__ void load(const uint8_t* sb, int grp) {
         g = grp;
-        hdr = ld_global<u32x4>(sb);
-        qa = ld_global<u32x4>(sb + 16 + 32 * grp);
-        qb = ld_global<u32x4>(sb + 32 + 32 * grp);
+        hdr = M::template ld<u32x4>(sb);
+        qa = M::template ld<u32x4>(sb + 16 + 32 * grp);
+        qb = M::template ld<u32x4>(sb + 32 + 32 * grp);
     }
     __device__ __forceinline__ void prepare() {
         const float d = f16_lo(hdr[0]);
         const float dmin = f16_hi(hdr[0]);
         // scales[12] = bytes 4..15 of the block = hdr[1..3]. Pair j < 4: scale = b[j] & 63,
         // min = b[j+4] & 63; pair j >= 4: scale = (b[j+4] & 15) | (b[j-4] >> 6) << 4,
-        // min = (b[j+4] >> 4) | (b[j] >> 6) << 4. Lane group g uses pairs 2g, 2g+1; both
-        // forms are computed and selected, so the unpacking has no divergent branch.
+        // min = (b[j+4] >> 4) | (b[j] >> 6) << 4. Lane group g uses pairs 2g, 2g+1. Both forms
+        // are one mask-and-shift recipe with per-lane constants (no divergent branch):
+        //   scale = (h & mh) | ((a >> sa) & ma),  min = ((h >> 4) & mh) | ((m >> sa) & ma)
+        // with a = b[j] / b[j-4], m = b[j+4] / b[j], h = b[j+4] (pairs 4-7 only), and
+        // (mh, sa, ma) = (0, 0, 63) for pairs 0-3, (15, 2, 48) for pairs 4-7, since
+        // (x >> 2) & 48 == (x >> 6) << 4 for a byte x.
         const uint32_t lo4 = hdr[1], mid4 = hdr[2], hi4 = hdr[3];  // bytes 0-3, 4-7, 8-11
-        const int sh0 = 16 * (g & 1), sh1 = sh0 + 8;                // byte (2g mod 4), +1
-        const uint32_t a0 = (lo4 >> sh0) & 0xffu, a1 = (lo4 >> sh1) & 0xffu;   // b[j], j in 0..3
-        const uint32_t m0 = (mid4 >> sh0) & 0xffu, m1 = (mid4 >> sh1) & 0xffu; // b[j+4]
-        const uint32_t h0 = (hi4 >> sh0) & 0xffu, h1 = (hi4 >> sh1) & 0xffu;   // b[j+8]
-        const bool low = g < 2;
-        const uint32_t sc_lo = low ? (a0 & 63u) : ((h0 & 0xFu) | ((a0 >> 6) << 4));
-        const uint32_t mn_lo = low ? (m0 & 63u) : ((h0 >> 4) | ((m0 >> 6) << 4));
-        const uint32_t sc_hi = low ? (a1 & 63u) : ((h1 & 0xFu) | ((a1 >> 6) << 4));
-        const uint32_t mn_hi = low ? (m1 & 63u) : ((h1 >> 4) | ((m1 >> 6) << 4));
+        const uint32_t sh0 = 16u * (uint32_t(g) & 1u);              // byte (2g mod 4); +8 for the pair's second
+        const uint32_t up = uint32_t(g) >> 1;                       // 0: pairs 0-3, 1: pairs 4-7
+        const uint32_t mh = 15u * up, sa = 2u * up, ma = 63u - 15u * up;
+        const uint32_t a0 = lo4 >> sh0, a1 = lo4 >> (sh0 + 8u);      // b[j] or b[j-4] in the low byte
+        const uint32_t m0 = mid4 >> sh0, m1 = mid4 >> (sh0 + 8u);    // b[j+4] or b[j]
+        const uint32_t h0 = hi4 >> sh0, h1 = hi4 >> (sh0 + 8u);      // b[j+4] for pairs 4-7
+        const uint32_t sc_lo = (h0 & mh) | ((a0 >> sa) & ma);
+        const uint32_t mn_lo = ((h0 >> 4) & mh) | ((m0 >> sa) & ma);
+        const uint32_t sc_hi = (h1 & mh) | ((a1 >> sa) & ma);
+        const uint32_t mn_hi = ((h1 >> 4) & mh) | ((m1 >> sa) & ma);
         d_lo = d * float(sc_lo); m_lo = -(dmin * float(mn_lo));
         d_hi = d * float(sc_hi); m_hi = -(dmin * float(mn_hi));
     }
@@ -154,10 +182,11 @@ __device__ __forceinline__ half2v q80_pair(uint32_t u, uint32_t sel, half2v dd) 
 }
 struct FragQ80 {
     uint32_t w[17];
+    template <class M = FromGlobal>
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
         const uint8_t* p = slab + 68 * g;
 #pragma unroll
-        for (int i = 0; i < 17; ++i) w[i] = ld_global<uint32_t>(p + 4 * i);
+        for (int i = 0; i < 17; ++i) w[i] = M::template ld<uint32_t>(p + 4 * i);
     }
     __device__ __forceinline__ void prepare() {}
     // Block b (0/1) occupies bytes 34b .. 34b+33 of the 68: d at 34b, q at 34b+2.
@@ -186,13 +215,17 @@ struct FragQ2K {
     uint32_t sc, dd;
     float d, dmin;
     int jbase;
+    template <class M = FromGlobal>
     __device__ __forceinline__ void load(const uint8_t* sb, int g) {
         const int n = g >> 1;
         jbase = 2 * (g & 1);
-        qa = ld_global<u32x4>(sb + 16 + 32 * n);
-        qb = ld_global<u32x4>(sb + 32 + 32 * n);
-        sc = ld_global<uint32_t>(sb + 8 * n + 2 * jbase);
-        dd = ld_global<uint32_t>(sb + 80);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // dword reads: an 84-byte slab staged in LDS is only 4-byte aligned
+            qa[i] = M::template ld<uint32_t>(sb + 16 + 32 * n + 4 * i);
+            qb[i] = M::template ld<uint32_t>(sb + 32 + 32 * n + 4 * i);
+        }
+        sc = M::template ld<uint32_t>(sb + 8 * n + 2 * jbase);
+        dd = M::template ld<uint32_t>(sb + 80);
     }
     __device__ __forceinline__ void prepare() {
         d = f16_lo(dd);
@@ -215,9 +248,10 @@ struct FragQ2K {
 // F16 rows: group g owns values [64g, 64g+64) as 8 x 16-byte fragments.
 struct FragF16 {
     half8 v[8];
+    template <class M = FromGlobal>
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = ld_global<half8>(slab + 128 * g + 16 * i);
+        for (int i = 0; i < 8; ++i) v[i] = M::template ld<half8>(slab + 128 * g + 16 * i);
     }
     __device__ __forceinline__ void prepare() {}
     __device__ __forceinline__ half8 step(int s) const { return v[s]; }
@@ -226,9 +260,10 @@ struct FragF16 {
 // BF16 rows, widened exactly to F32 and rounded once to F16.
 struct FragBF16 {
     u32x4 v[8];
+    template <class M = FromGlobal>
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = ld_global<u32x4>(slab + 128 * g + 16 * i);
+        for (int i = 0; i < 8; ++i) v[i] = M::template ld<u32x4>(slab + 128 * g + 16 * i);
     }
     __device__ __forceinline__ void prepare() {}
     __device__ __forceinline__ half8 step(int s) const {

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
             const uint32_t a = a0 + 16u * rb + 4u * gq + i;
             if (a >= a1) continue;
             if (MODE == kGateUp) {
-                g.out_h[uint64_t(a) * g.n_out + col0] = half_sat(silu(acc0[rb][i]) * acc1[rb][i]);
+                g.out_h[uint64_t(a) * g.n_out + col0] = half_sat(silu_fast(acc0[rb][i]) * acc1[rb][i]);
             } else {
                 const uint32_t d = uint32_t(g.dst[a]);
                 if (d < N) {
@@ -227,6 +227,294 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
                 }
             }
         }
+}
+
+// ---------------------------------------------------------------------------------------
+// Routed products, v2: 512-thread workgroups (8 waves) over a 64-row tile and `npi`
+// consecutive column tiles of 256 weight columns (gate/up: 128 gate + 128 up columns = 128
+// hidden columns; down: 256 output columns). The activation slab (64 rows x 256 values)
+// is copied global -> LDS by the load unit (global_load_lds_dwordx4) into a double-buffered,
+// XOR-swizzled ring, so staging costs no registers and one barrier per slab; each lane's
+// raw weight fragments for the next step are in flight in registers while the current
+// step decodes and multiplies. (column tile, slab) steps of the workgroup form one flat
+// pipeline, so short reductions (down: K = I) do not drain it between column tiles.
+// ---------------------------------------------------------------------------------------
+constexpr int kV2Threads = 512;
+constexpr int kV2Cols = 256;
+
+// Position (in 16-byte chunks) of chunk c of row r inside a swizzled 64 x 256 slab: the
+// 16 rows one MFMA A-fragment read touches map to 16 distinct 4-bank groups.
+__device__ __forceinline__ uint32_t a_pos(uint32_t r, uint32_t c) { return r * 32u + (c ^ (r & 15u)); }
+
+template <int MODE>
+__device__ void zero_cols(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_t c0, uint32_t c1, bool by_dst) {
+    const uint32_t width = c1 - c0;
+    for (uint32_t i = threadIdx.x; i < 64u * width; i += kV2Threads) {
+        const uint32_t r = r0 + i / width, c = c0 + i % width;
+        if (r >= r1 || r >= g.n_entries) continue;
+        if (MODE == kGateUp) {
+            g.out_h[uint64_t(r) * g.n_out + c] = _Float16(0.0f);
+        } else if (!by_dst) {
+            g.out_f[uint64_t(r) * g.n_out + c] = 0.0f;
+        } else {
+            const uint32_t d = uint32_t(g.dst[r]);
+            if (d < g.n_entries) g.out_f[uint64_t(d) * g.n_out + c] = 0.0f;
+            else atomicOr(g.status, 2u);
+        }
+    }
+}
+
+// The work item of one v2 workgroup: tile rows [a0, a1) of one expert group and column
+// tiles [nt_begin, nt_end), with the expert's two weight matrices.
+struct TileWork {
+    uint32_t a0, a1, nt_begin, nt_end;
+    const uint8_t* w0;
+    const uint8_t* w1;
+};
+
+// Shared prologue of the v2 kernels: reads the status word and the plan's tile count once,
+// maps the workgroup to its item over the real tiles (XCD-aware), and validates the tile
+// against the plan. Returns false when the workgroup has nothing (more) to do; failed
+// tiles have written their zeros and status bits by then. Every thread of the workgroup
+// takes the same branch.
+template <int MODE>
+__device__ bool v2_prologue(const RoutedGemm& g, uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks, TileWork& t) {
+    __shared__ uint32_t s_flag, s_tiles;
+    const Plan* p = g.plan;
+    const uint32_t out_per_nt = MODE == kGateUp ? kV2Cols / 2 : kV2Cols;  // output columns per column tile
+    if (threadIdx.x == 0) {
+        s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_tiles = p->n_tiles;
+    }
+    __syncthreads();
+    if (s_flag & 2u) {  // invalid plan or permutation: every tile slot writes zeros
+        if (blockIdx.x >= g.tile_capacity * n_chunks) return false;
+        const uint32_t ti = blockIdx.x / n_chunks, ch = blockIdx.x % n_chunks;
+        const uint32_t nb = ch * npi, ne = nb + npi < n_ntiles ? nb + npi : n_ntiles;
+        zero_cols<MODE>(g, ti * 64u, ti * 64u + 64u, nb * out_per_nt, ne * out_per_nt, false);
+        return false;
+    }
+    const uint32_t real = (s_tiles < g.tile_capacity ? s_tiles : g.tile_capacity) * n_chunks;
+    const uint32_t w = xcd_remap(blockIdx.x, real);
+    if (w >= real) return false;
+    const uint32_t tile_index = w / n_chunks, chunk = w % n_chunks;
+    t.nt_begin = chunk * npi;
+    t.nt_end = t.nt_begin + npi < n_ntiles ? t.nt_begin + npi : n_ntiles;
+    const uint32_t tg = g.tiles[2 * tile_index], a0 = g.tiles[2 * tile_index + 1];
+    bool ok = tg < p->n_groups;
+    uint32_t gend = 0;
+    int32_t ex = -1;
+    if (ok) {
+        const int32_t f = p->grp_start[tg], e = p->grp_start[tg + 1];
+        ex = p->grp_e[tg];
+        ok = f >= 0 && e > f && uint32_t(e) <= p->n_entries && ex >= 0 && uint32_t(ex) < g.n_experts;
+        if (ok) {
+            gend = uint32_t(e);
+            ok = a0 >= uint32_t(f) && a0 < gend && (a0 - uint32_t(f)) % 64u == 0u;
+        }
+    }
+    if (!ok) {
+        if (threadIdx.x == 0) atomicOr(g.status, 2u);
+        zero_cols<MODE>(g, tile_index * 64u, tile_index * 64u + 64u, t.nt_begin * out_per_nt,
+                        t.nt_end * out_per_nt, false);
+        return false;
+    }
+    t.a0 = a0;
+    t.a1 = a0 + 64u < gend ? a0 + 64u : gend;
+    const uint64_t* addr = g.addresses + 3u * uint32_t(ex);
+    t.w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
+    t.w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
+    if (t.w0 == nullptr || t.w1 == nullptr) {
+        if (threadIdx.x == 0) atomicOr(g.status, 1u);
+        zero_cols<MODE>(g, t.a0, t.a1, t.nt_begin * out_per_nt, t.nt_end * out_per_nt, MODE == kDown);
+        return false;
+    }
+    return true;
+}
+
+// Activation copy map of one 64 x 256 slab: wave instruction q = 4*wave + j (j = 0..3)
+// fills chunk positions [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk
+// C = (lane & 31) ^ (R & 15). Rows past the tile's end repeat its last row.
+__device__ __forceinline__ void slab_sources(const RoutedGemm& g, const TileWork& t, int wave, int lane,
+                                             const _Float16* (&asrc)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t R = 2u * (4u * wave + j) + (uint32_t(lane) >> 5);
+        const uint32_t C = (uint32_t(lane) & 31u) ^ (R & 15u);
+        uint32_t row = t.a0 + R;
+        if (row > t.a1 - 1u) row = t.a1 - 1u;
+        asrc[j] = g.a + uint64_t(row) * g.k + 8u * C;
+    }
+}
+
+// Issues the four LDS-DMA copies (16 B per lane) of this wave's share of the slab at k0.
+__device__ __forceinline__ void issue_slab(const _Float16* const (&asrc)[4], uint32_t k0, _Float16* slab, int wave) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(asrc[j] + k0)),
+            reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(slab + (4 * wave + j) * 512)),
+            16, 0, 0);
+}
+
+// One 256-value slab of the wave's 64 x 32 block: A fragments from the swizzled LDS slab,
+// B fragments decoded from the two weight fragments.
+template <class Frag>
+__device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag& c0, const Frag& c1,
+                                         float4v (&acc0)[4], float4v (&acc1)[4]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const half8 b0 = c0.step(s), b1 = c1.step(s);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const half8 a = *reinterpret_cast<const half8*>(buf + 8u * a_pos(16u * rb + n, 8u * gq + s));
+            acc0[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b0, acc0[rb], 0, 0, 0);
+            acc1[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc1[rb], 0, 0, 0);
+        }
+    }
+}
+
+// Writes a finished column tile and clears the accumulators. gate/up: eh[a][col0] =
+// half_sat(silu(gate) * up); down: parts[dst[a]][col0 | col1], with a destination outside
+// [0, N) reported (status bit 1) and the entry's own row zeroed instead.
+template <int MODE>
+__device__ __forceinline__ void v2_epilogue(const RoutedGemm& g, const uint32_t* s_dst, uint32_t a0, uint32_t a1,
+                                            int gq, uint32_t col0, uint32_t col1, float4v (&acc0)[4],
+                                            float4v (&acc1)[4]) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = a0 + 16u * rb + 4u * gq + i;
+            if (a >= a1) continue;
+            if (MODE == kGateUp) {
+                g.out_h[uint64_t(a) * g.n_out + col0] = half_sat(silu_fast(acc0[rb][i]) * acc1[rb][i]);
+            } else {
+                const uint32_t d = s_dst[16 * rb + 4 * gq + i];
+                if (d < g.n_entries) {
+                    g.out_f[uint64_t(d) * g.n_out + col0] = acc0[rb][i];
+                    g.out_f[uint64_t(d) * g.n_out + col1] = acc1[rb][i];
+                } else {
+                    atomicOr(g.status, 2u);
+                    g.out_f[uint64_t(a) * g.n_out + col0] = 0.0f;
+                    g.out_f[uint64_t(a) * g.n_out + col1] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
+}
+
+// Weight column of lane n in wave `wave` for column tile nt: gate/up pairs gate and up rows
+// j (the same j in both matrices); down covers 256 output columns, 32 per wave.
+template <int MODE>
+__device__ __forceinline__ uint32_t v2_col(uint32_t nt, int wave, int n, int which) {
+    if (MODE == kGateUp) return nt * 128u + 16u * wave + n;
+    return nt * 256u + 32u * wave + 16u * which + n;
+}
+
+// Bytes moved per lane by one LDS-DMA copy of weight-row slabs: 16 where the slab size
+// allows, else 4 (Q2_K's 84-byte slabs). Lane l of a copy writes at LDS base + l * size.
+template <int SB> struct ChunkBytes { static constexpr int value = SB % 16 == 0 ? 16 : 4; };
+
+// Copies slab sb of the workgroup's 256 weight rows for column tile nt into `wbuf`, packed
+// as [256 rows][SB bytes], by LDS-DMA: wave instruction q moves the 64 consecutive chunks
+// [64q, 64q + 64) of that packed image, so each instruction reads a few whole row slabs
+// (contiguous bytes) instead of 64 scattered fragments. gate/up: rows 0-127 are gate rows
+// nt*128 + r, rows 128-255 up rows; down: rows nt*256 + r.
+template <class Frag, int MODE>
+__device__ __forceinline__ void issue_weights(const RoutedGemm& g, const TileWork& t, uint32_t nt, uint32_t sb,
+                                              uint8_t* wbuf, int wave, int lane) {
+    constexpr int SB = SlabBytes<Frag>::value;
+    constexpr int CS = ChunkBytes<SB>::value;
+    constexpr uint32_t kPerRow = SB / CS, kTotal = 256u * kPerRow, kInstr = (kTotal + 63u) / 64u;
+    for (uint32_t q = uint32_t(wave); q < kInstr; q += kV2Threads / 64) {
+        const uint32_t c = 64u * q + uint32_t(lane);
+        if (c < kTotal) {
+            const uint32_t r = c / kPerRow, piece = c % kPerRow;
+            const uint8_t* src;
+            if (MODE == kGateUp) src = (r < 128u ? t.w0 + uint64_t(nt * 128u + r) * g.row_bytes
+                                                  : t.w1 + uint64_t(nt * 128u + r - 128u) * g.row_bytes);
+            else src = t.w0 + uint64_t(nt * 256u + r) * g.row_bytes;
+            src += uint64_t(sb) * SB + piece * CS;
+            auto* gsrc = reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(src));
+            auto* ldst = reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(wbuf + q * 64u * CS));
+            if constexpr (CS == 16) __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
+            else __builtin_amdgcn_global_load_lds(gsrc, ldst, 4, 0, 0);
+        }
+    }
+}
+
+// Packed-image row of lane n's fragment `which` in wave `wave` (see issue_weights).
+template <int MODE>
+__device__ __forceinline__ uint32_t staged_row(int wave, int n, int which) {
+    if (MODE == kGateUp) return 128u * which + 16u * wave + n;
+    return 32u * wave + 16u * which + n;
+}
+
+// Routed products: 512-thread workgroups (8 waves) over a 64-row tile and `npi`
+// consecutive column tiles of 256 weight rows (gate/up: 128 gate + 128 up rows = 128
+// hidden columns; down: 256 output columns). Per (column tile, slab) step, the activation
+// slab and the 256 weight-row slabs are copied global -> LDS by LDS-DMA one step ahead;
+// each lane then reads its weight fragments from LDS, decodes them into the MFMA B layout
+// and multiplies against A fragments from the swizzled activation slab. WBUF = 2
+// double-buffers the weight image (one barrier per step); WBUF = 1 (Q8_0, whose image is
+// 68 KB) reads the fragments to registers and takes a second barrier before refilling it.
+// The steps of a workgroup form one flat pipeline, so short reductions (down: K = I) do
+// not drain it between column tiles.
+// RESIDENT (K <= 512): both activation slabs are copied once and stay in LDS for all of
+// the workgroup's column tiles, instead of being re-read from L2 for each of them.
+template <class Frag, int MODE, int WBUF, bool RESIDENT>
+__global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGemm g, uint32_t n_ntiles, uint32_t npi,
+                                                                        uint32_t n_chunks) {
+    constexpr int SB = SlabBytes<Frag>::value;
+    constexpr uint32_t kWBytes = 256u * SB;
+    __shared__ __attribute__((aligned(1024))) _Float16 sa[2][64 * kSlab];
+    __shared__ __attribute__((aligned(1024))) uint8_t sw[WBUF][kWBytes];
+    __shared__ uint32_t s_dst[64];  // down: destination row of each tile row
+    TileWork t;
+    if (!v2_prologue<MODE>(g, n_ntiles, npi, n_chunks, t)) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, gq = lane >> 4;
+    // Read once here rather than in each epilogue, where a dependent global load would also
+    // wait for the copies of the next step (visible after the first loop barrier).
+    if (MODE == kDown && tid < 64) s_dst[tid] = t.a0 + uint32_t(tid) < t.a1 ? uint32_t(g.dst[t.a0 + tid]) : ~0u;
+    const uint32_t n_slabs = g.k / kSlab;
+    const uint32_t n_steps = (t.nt_end - t.nt_begin) * n_slabs;
+    const _Float16* asrc[4];
+    slab_sources(g, t, wave, lane, asrc);
+    auto issue = [&](uint32_t step) {
+        const uint32_t nt = t.nt_begin + step / n_slabs, sb = step % n_slabs;
+        if (!RESIDENT) issue_slab(asrc, sb * kSlab, sa[step & 1u], wave);
+        issue_weights<Frag, MODE>(g, t, nt, sb, sw[WBUF == 2 ? (step & 1u) : 0u], wave, lane);
+    };
+    if (RESIDENT)
+        for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
+    float4v acc0[4], acc1[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
+    issue(0);
+    for (uint32_t step = 0; step < n_steps; ++step) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
+        __syncthreads();                                       // ... from every wave
+        const bool more = step + 1 < n_steps;
+        const uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
+        Frag c0, c1;
+        c0.template load<FromLds>(wb + staged_row<MODE>(wave, n, 0) * SB, gq);
+        c1.template load<FromLds>(wb + staged_row<MODE>(wave, n, 1) * SB, gq);
+        // A barrier waits for every outstanding load of the wave, so with one weight image
+        // the next step's copies are issued only after the second barrier.
+        if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
+        if (more) issue(step + 1);
+        c0.prepare();
+        c1.prepare();
+        const uint32_t sb = step % n_slabs;
+        slab_mma(sa[RESIDENT ? sb : (step & 1u)], n, gq, c0, c1, acc0, acc1);
+        if (sb == n_slabs - 1u) {  // column tile complete
+            const uint32_t nt = t.nt_begin + step / n_slabs;
+            v2_epilogue<MODE>(g, s_dst, t.a0, t.a1, gq, v2_col<MODE>(nt, wave, n, 0), v2_col<MODE>(nt, wave, n, 1),
+                              acc0, acc1);
+        }
+    }
 }
 
 // Dense (shared-expert) products: rows are tokens in 64-row tiles.
@@ -258,7 +546,7 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseGemm g, uint32_t n
             const uint32_t r = r0 + 16u * rb + 4u * gq + i;
             if (r >= r1) continue;
             if (MODE == kGateUp) {
-                g.out_h[uint64_t(r) * g.n_out + col0] = half_sat(silu(acc0[rb][i]) * acc1[rb][i]);
+                g.out_h[uint64_t(r) * g.n_out + col0] = half_sat(silu_fast(acc0[rb][i]) * acc1[rb][i]);
             } else {
                 g.out_f[uint64_t(r) * g.n_out + col0] = acc0[rb][i];
                 g.out_f[uint64_t(r) * g.n_out + col1] = acc1[rb][i];
@@ -288,6 +576,24 @@ __global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restr
 
 template <class Frag, int MODE>
 hipError_t launch_routed(const RoutedGemm& g, hipStream_t s) {
+    const uint32_t out_per_v2 = MODE == kGateUp ? kV2Cols / 2 : kV2Cols;
+    if (g.k % kSlab == 0 && g.n_out % out_per_v2 == 0) {
+        const uint32_t n_ntiles = g.n_out / out_per_v2;
+        // About 8 (column tile, slab) steps per workgroup.
+        const uint32_t n_slabs = g.k / kSlab;
+        uint32_t npi = n_slabs >= 8 ? 1u : 8u / n_slabs;
+        if (npi > n_ntiles) npi = n_ntiles;
+        const uint32_t n_chunks = (n_ntiles + npi - 1) / npi;
+        const uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
+        // Two weight images fit beside the activation double buffer unless a slab image is
+        // larger than 40 KB (Q8_0: 68 KB).
+        constexpr int kWBuf = 256 * SlabBytes<Frag>::value <= 40960 ? 2 : 1;
+        if (n_slabs <= 2)
+            routed_gemm_staged_kernel<Frag, MODE, kWBuf, true><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
+        else
+            routed_gemm_staged_kernel<Frag, MODE, kWBuf, false><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
+        return hipGetLastError();
+    }
     const uint32_t n_ntiles = MODE == kGateUp ? g.n_out / 64u : g.n_out / 128u;
     const uint32_t total = g.tile_capacity * n_ntiles;
     const uint32_t blocks = (total + 7u) & ~7u;
