@@ -230,17 +230,18 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
 }
 
 // ---------------------------------------------------------------------------------------
-// Routed products, v2: 512-thread workgroups (8 waves) over a 64-row tile and `npi`
-// consecutive column tiles of 256 weight columns (gate/up: 128 gate + 128 up columns = 128
-// hidden columns; down: 256 output columns). The activation slab (64 rows x 256 values)
-// is copied global -> LDS by the load unit (global_load_lds_dwordx4) into a double-buffered,
-// XOR-swizzled ring, so staging costs no registers and one barrier per slab; each lane's
-// raw weight fragments for the next step are in flight in registers while the current
-// step decodes and multiplies. (column tile, slab) steps of the workgroup form one flat
-// pipeline, so short reductions (down: K = I) do not drain it between column tiles.
+// Routed products, staged: 512-thread workgroups (8 waves) over a 64-row tile and `npi`
+// consecutive column tiles. Each wave owns NF 16-column weight fragments (NF = 2 or 4) and
+// all 64 rows, so one column tile covers 128*NF weight rows (gate/up: 64*NF gate rows and
+// the 64*NF up rows of the same hidden columns; down: 128*NF output columns). Per (column
+// tile, slab) step the 64 x 256 activation slab and the weight-row slabs are copied
+// global -> LDS by LDS-DMA (global_load_lds), one step ahead and interleaved with the
+// multiplies; lanes then read their raw fragments from LDS, decode them into the MFMA B
+// layout and multiply against A fragments from the XOR-swizzled activation slab. The steps
+// of a workgroup form one flat pipeline, so short reductions (down: K = I) do not drain it
+// between column tiles.
 // ---------------------------------------------------------------------------------------
 constexpr int kV2Threads = 512;
-constexpr int kV2Cols = 256;
 
 // Position (in 16-byte chunks) of chunk c of row r inside a swizzled 64 x 256 slab: the
 // 16 rows one MFMA A-fragment read touches map to 16 distinct 4-bank groups.
@@ -264,7 +265,7 @@ __device__ void zero_cols(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_
     }
 }
 
-// The work item of one v2 workgroup: tile rows [a0, a1) of one expert group and column
+// The work item of one staged workgroup: tile rows [a0, a1) of one expert group and column
 // tiles [nt_begin, nt_end), with the expert's two weight matrices.
 struct TileWork {
     uint32_t a0, a1, nt_begin, nt_end;
@@ -272,16 +273,16 @@ struct TileWork {
     const uint8_t* w1;
 };
 
-// Shared prologue of the v2 kernels: reads the status word and the plan's tile count once,
+// Shared prologue of the staged kernels: reads the status word and the plan's tile count once,
 // maps the workgroup to its item over the real tiles (XCD-aware), and validates the tile
 // against the plan. Returns false when the workgroup has nothing (more) to do; failed
 // tiles have written their zeros and status bits by then. Every thread of the workgroup
 // takes the same branch.
 template <int MODE>
-__device__ bool v2_prologue(const RoutedGemm& g, uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks, TileWork& t) {
+__device__ bool v2_prologue(const RoutedGemm& g, uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks,
+                            uint32_t out_per_nt, TileWork& t) {
     __shared__ uint32_t s_flag, s_tiles;
     const Plan* p = g.plan;
-    const uint32_t out_per_nt = MODE == kGateUp ? kV2Cols / 2 : kV2Cols;  // output columns per column tile
     if (threadIdx.x == 0) {
         s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_tiles = p->n_tiles;
@@ -347,40 +348,70 @@ __device__ __forceinline__ void slab_sources(const RoutedGemm& g, const TileWork
     }
 }
 
-// Issues the four LDS-DMA copies (16 B per lane) of this wave's share of the slab at k0.
+// Issues LDS-DMA copy j (0..3, 16 B per lane) of this wave's share of the slab at k0.
+__device__ __forceinline__ void issue_slab_part(const _Float16* const (&asrc)[4], uint32_t k0, _Float16* slab,
+                                                int wave, int j) {
+    __builtin_amdgcn_global_load_lds(
+        reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(asrc[j] + k0)),
+        reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(slab + (4 * wave + j) * 512)),
+        16, 0, 0);
+}
 __device__ __forceinline__ void issue_slab(const _Float16* const (&asrc)[4], uint32_t k0, _Float16* slab, int wave) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(asrc[j] + k0)),
-            reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(slab + (4 * wave + j) * 512)),
-            16, 0, 0);
+    for (int j = 0; j < 4; ++j) issue_slab_part(asrc, k0, slab, wave, j);
 }
 
-// One 256-value slab of the wave's 64 x 32 block: A fragments from the swizzled LDS slab,
-// B fragments decoded from the two weight fragments.
-template <class Frag>
-__device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag& c0, const Frag& c1,
-                                         float4v (&acc0)[4], float4v (&acc1)[4]) {
+// Geometry of a staged step with NF fragments per wave.
+template <int MODE, int NF>
+struct Staged {
+    static constexpr uint32_t kImageRows = 128u * NF;                          // weight rows per step
+    static constexpr uint32_t kHalf = 64u * NF;                                // gate/up: gate rows, then up rows
+    static constexpr uint32_t kOut = MODE == kGateUp ? 64u * NF : 128u * NF;   // output columns per column tile
+    // Column of lane n's fragment f within the column tile (gate/up: the hidden column, the
+    // same for gate fragment f and up fragment f + NF/2).
+    __device__ static __forceinline__ uint32_t col(int wave, int n, int f) {
+        if (MODE == kGateUp) return uint32_t(wave) * (8u * NF) + 16u * uint32_t(f % (NF / 2)) + uint32_t(n);
+        return uint32_t(wave) * (16u * NF) + 16u * uint32_t(f) + uint32_t(n);
+    }
+    // Row of the packed weight image holding that fragment.
+    __device__ static __forceinline__ uint32_t image_row(int wave, int n, int f) {
+        if (MODE == kGateUp) return (f < NF / 2 ? 0u : kHalf) + col(wave, n, f);
+        return col(wave, n, f);
+    }
+};
+
+// after_s(s) runs after k-step s: the staged kernel issues part s of the next step's copies
+// there, so a wave never blocks on a long burst of memory instructions while it could be
+// multiplying.
+template <class Frag, int NF, class After>
+__device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag (&c)[NF],
+                                         float4v (&acc)[NF][4], After after_s) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const half8 b0 = c0.step(s), b1 = c1.step(s);
+        half8 b[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) b[f] = c[f].step(s);
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             const half8 a = *reinterpret_cast<const half8*>(buf + 8u * a_pos(16u * rb + n, 8u * gq + s));
-            acc0[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b0, acc0[rb], 0, 0, 0);
-            acc1[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc1[rb], 0, 0, 0);
+#pragma unroll
+            for (int f = 0; f < NF; ++f) acc[f][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[f], acc[f][rb], 0, 0, 0);
         }
+        after_s(s);
+        // Keep each k-step's decode next to its multiplies: hoisting the decodes of later
+        // k-steps ahead would hold NF x 4 decoded registers per k-step at once. The next
+        // k-step's decode still overlaps the multiplies in flight.
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// Writes a finished column tile and clears the accumulators. gate/up: eh[a][col0] =
-// half_sat(silu(gate) * up); down: parts[dst[a]][col0 | col1], with a destination outside
-// [0, N) reported (status bit 1) and the entry's own row zeroed instead.
-template <int MODE>
-__device__ __forceinline__ void v2_epilogue(const RoutedGemm& g, const uint32_t* s_dst, uint32_t a0, uint32_t a1,
-                                            int gq, uint32_t col0, uint32_t col1, float4v (&acc0)[4],
-                                            float4v (&acc1)[4]) {
+// Writes a finished column tile and clears the accumulators. gate/up: eh[a][col] =
+// half_sat(silu(gate) * up); down: parts[dst[a]][col], with a destination outside [0, N)
+// reported (status bit 1) and the entry's own row zeroed instead.
+template <int MODE, int NF>
+__device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint32_t* s_dst, uint32_t a0, uint32_t a1,
+                                                uint32_t col0, int wave, int n, int gq, float4v (&acc)[NF][4]) {
+    using S = Staged<MODE, NF>;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -388,92 +419,98 @@ __device__ __forceinline__ void v2_epilogue(const RoutedGemm& g, const uint32_t*
             const uint32_t a = a0 + 16u * rb + 4u * gq + i;
             if (a >= a1) continue;
             if (MODE == kGateUp) {
-                g.out_h[uint64_t(a) * g.n_out + col0] = half_sat(silu_fast(acc0[rb][i]) * acc1[rb][i]);
+#pragma unroll
+                for (int f = 0; f < NF / 2; ++f)
+                    g.out_h[uint64_t(a) * g.n_out + col0 + S::col(wave, n, f)] =
+                        half_sat(silu_fast(acc[f][rb][i]) * acc[f + NF / 2][rb][i]);
             } else {
                 const uint32_t d = s_dst[16 * rb + 4 * gq + i];
-                if (d < g.n_entries) {
-                    g.out_f[uint64_t(d) * g.n_out + col0] = acc0[rb][i];
-                    g.out_f[uint64_t(d) * g.n_out + col1] = acc1[rb][i];
-                } else {
-                    atomicOr(g.status, 2u);
-                    g.out_f[uint64_t(a) * g.n_out + col0] = 0.0f;
-                    g.out_f[uint64_t(a) * g.n_out + col1] = 0.0f;
-                }
+                const bool good = d < g.n_entries;
+                if (!good) atomicOr(g.status, 2u);
+                const uint64_t row = good ? d : a;
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    g.out_f[row * g.n_out + col0 + S::col(wave, n, f)] = good ? acc[f][rb][i] : 0.0f;
             }
         }
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
-}
-
-// Weight column of lane n in wave `wave` for column tile nt: gate/up pairs gate and up rows
-// j (the same j in both matrices); down covers 256 output columns, 32 per wave.
-template <int MODE>
-__device__ __forceinline__ uint32_t v2_col(uint32_t nt, int wave, int n, int which) {
-    if (MODE == kGateUp) return nt * 128u + 16u * wave + n;
-    return nt * 256u + 32u * wave + 16u * which + n;
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
 }
 
 // Bytes moved per lane by one LDS-DMA copy of weight-row slabs: 16 where the slab size
 // allows, else 4 (Q2_K's 84-byte slabs). Lane l of a copy writes at LDS base + l * size.
 template <int SB> struct ChunkBytes { static constexpr int value = SB % 16 == 0 ? 16 : 4; };
 
-// Copies slab sb of the workgroup's 256 weight rows for column tile nt into `wbuf`, packed
-// as [256 rows][SB bytes], by LDS-DMA: wave instruction q moves the 64 consecutive chunks
-// [64q, 64q + 64) of that packed image, so each instruction reads a few whole row slabs
-// (contiguous bytes) instead of 64 scattered fragments. gate/up: rows 0-127 are gate rows
-// nt*128 + r, rows 128-255 up rows; down: rows nt*256 + r.
-template <class Frag, int MODE>
-__device__ __forceinline__ void issue_weights(const RoutedGemm& g, const TileWork& t, uint32_t nt, uint32_t sb,
-                                              uint8_t* wbuf, int wave, int lane) {
-    constexpr int SB = SlabBytes<Frag>::value;
-    constexpr int CS = ChunkBytes<SB>::value;
-    constexpr uint32_t kPerRow = SB / CS, kTotal = 256u * kPerRow, kInstr = (kTotal + 63u) / 64u;
-    for (uint32_t q = uint32_t(wave); q < kInstr; q += kV2Threads / 64) {
-        const uint32_t c = 64u * q + uint32_t(lane);
-        if (c < kTotal) {
-            const uint32_t r = c / kPerRow, piece = c % kPerRow;
-            const uint8_t* src;
-            if (MODE == kGateUp) src = (r < 128u ? t.w0 + uint64_t(nt * 128u + r) * g.row_bytes
-                                                  : t.w1 + uint64_t(nt * 128u + r - 128u) * g.row_bytes);
-            else src = t.w0 + uint64_t(nt * 256u + r) * g.row_bytes;
-            src += uint64_t(sb) * SB + piece * CS;
-            auto* gsrc = reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(src));
-            auto* ldst = reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(wbuf + q * 64u * CS));
-            if constexpr (CS == 16) __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
-            else __builtin_amdgcn_global_load_lds(gsrc, ldst, 4, 0, 0);
+// The weight-row slabs of one (column tile, slab) step are copied into an LDS image packed
+// as [128*NF rows][SB bytes] by LDS-DMA: wave instruction q moves the 64 consecutive chunks
+// [64q, 64q + 64) of that image, so each instruction reads a few whole row slabs
+// (contiguous bytes) instead of 64 scattered fragments. gate/up: image rows [0, 64*NF) are
+// gate rows nt*64*NF + r, the rest the up rows of the same hidden columns; down: rows
+// nt*128*NF + r. Every instruction is full (128*NF rows x SB/CS chunks is a multiple of 64)
+// and lies wholly in the gate or the up half. Wave w issues instructions q = w + 8j;
+// `off` keeps each lane's byte offset within its matrix for column tile 0, slab 0.
+template <class Frag, int MODE, int NF>
+struct WeightCopy {
+    static constexpr int SB = SlabBytes<Frag>::value;
+    static constexpr int CS = ChunkBytes<SB>::value;
+    static constexpr uint32_t kPerRow = SB / CS;
+    static constexpr uint32_t kInstr = Staged<MODE, NF>::kImageRows * kPerRow / 64u;
+    static constexpr uint32_t kPerWave = (kInstr + 7u) / 8u;
+    static_assert((Staged<MODE, NF>::kImageRows * kPerRow) % 128u == 0u, "copies must be whole wave instructions");
+    uint32_t off[kPerWave];
+    __device__ __forceinline__ void init(const RoutedGemm& g, int wave, int lane) {
+#pragma unroll
+        for (uint32_t j = 0; j < kPerWave; ++j) {
+            const uint32_t c = 64u * (uint32_t(wave) + 8u * j) + uint32_t(lane);
+            uint32_t r = c / kPerRow;
+            const uint32_t piece = c - r * kPerRow;
+            if (MODE == kGateUp && r >= Staged<MODE, NF>::kHalf) r -= Staged<MODE, NF>::kHalf;
+            off[j] = r * g.row_bytes + piece * CS;  // < 512 rows x row_bytes: 32 bits suffice
         }
     }
-}
+    // Issues item j (instruction q = wave + 8j) of the copy for (nt, sb) into `wbuf`.
+    __device__ __forceinline__ void issue(const RoutedGemm& g, const TileWork& t, uint32_t nt, uint32_t sb,
+                                          uint8_t* wbuf, int wave, uint32_t j) const {
+        const uint32_t q = uint32_t(wave) + 8u * j;
+        if (q >= kInstr) return;
+        const bool up = MODE == kGateUp && q >= kInstr / 2u;
+        const uint8_t* base = up ? t.w1 : t.w0;
+        const uint32_t rows_per_tile = MODE == kGateUp ? Staged<MODE, NF>::kHalf : Staged<MODE, NF>::kImageRows;
+        const uint64_t tile_off = uint64_t(nt) * rows_per_tile * g.row_bytes + uint64_t(sb) * SB;
+        const uint8_t* src = base + tile_off + off[j];
+        auto* gsrc = reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(src));
+        auto* ldst = reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(wbuf + q * 64u * CS));
+        if constexpr (CS == 16) __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
+        else __builtin_amdgcn_global_load_lds(gsrc, ldst, 4, 0, 0);
+    }
+};
 
-// Packed-image row of lane n's fragment `which` in wave `wave` (see issue_weights).
-template <int MODE>
-__device__ __forceinline__ uint32_t staged_row(int wave, int n, int which) {
-    if (MODE == kGateUp) return 128u * which + 16u * wave + n;
-    return 32u * wave + 16u * which + n;
-}
+// Weight images per workgroup: two (one filled while the other is read) when they fit
+// beside the activation double buffer within 140 KB of LDS, else one, read into registers
+// behind a second barrier before it is refilled.
+template <class Frag, int NF>
+struct StagedBuffers {
+    static constexpr uint32_t kImage = 128u * NF * SlabBytes<Frag>::value;
+    static constexpr int kWBuf = 65536u + 2u * kImage <= 143360u ? 2 : 1;
+    static_assert(65536u + kImage <= 143360u, "weight image too large for LDS");
+};
 
-// Routed products: 512-thread workgroups (8 waves) over a 64-row tile and `npi`
-// consecutive column tiles of 256 weight rows (gate/up: 128 gate + 128 up rows = 128
-// hidden columns; down: 256 output columns). Per (column tile, slab) step, the activation
-// slab and the 256 weight-row slabs are copied global -> LDS by LDS-DMA one step ahead;
-// each lane then reads its weight fragments from LDS, decodes them into the MFMA B layout
-// and multiplies against A fragments from the swizzled activation slab. WBUF = 2
-// double-buffers the weight image (one barrier per step); WBUF = 1 (Q8_0, whose image is
-// 68 KB) reads the fragments to registers and takes a second barrier before refilling it.
-// The steps of a workgroup form one flat pipeline, so short reductions (down: K = I) do
-// not drain it between column tiles.
 // RESIDENT (K <= 512): both activation slabs are copied once and stay in LDS for all of
 // the workgroup's column tiles, instead of being re-read from L2 for each of them.
-template <class Frag, int MODE, int WBUF, bool RESIDENT>
+template <class Frag, int MODE, int NF, bool RESIDENT>
 __global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGemm g, uint32_t n_ntiles, uint32_t npi,
                                                                         uint32_t n_chunks) {
+    using S = Staged<MODE, NF>;
+    using WC = WeightCopy<Frag, MODE, NF>;
     constexpr int SB = SlabBytes<Frag>::value;
-    constexpr uint32_t kWBytes = 256u * SB;
+    constexpr int WBUF = StagedBuffers<Frag, NF>::kWBuf;
     __shared__ __attribute__((aligned(1024))) _Float16 sa[2][64 * kSlab];
-    __shared__ __attribute__((aligned(1024))) uint8_t sw[WBUF][kWBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t sw[WBUF][StagedBuffers<Frag, NF>::kImage];
     __shared__ uint32_t s_dst[64];  // down: destination row of each tile row
     TileWork t;
-    if (!v2_prologue<MODE>(g, n_ntiles, npi, n_chunks, t)) return;
+    if (!v2_prologue<MODE>(g, n_ntiles, npi, n_chunks, S::kOut, t)) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, gq = lane >> 4;
     // Read once here rather than in each epilogue, where a dependent global load would also
     // wait for the copies of the next step (visible after the first loop barrier).
@@ -482,37 +519,46 @@ __global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGe
     const uint32_t n_steps = (t.nt_end - t.nt_begin) * n_slabs;
     const _Float16* asrc[4];
     slab_sources(g, t, wave, lane, asrc);
-    auto issue = [&](uint32_t step) {
+    WC wc;
+    wc.init(g, wave, lane);
+    // Part p (0..7) of the copies of `step`: activation copy p (p < 4, streamed slabs only)
+    // and weight items j with j % 8 == p.
+    auto issue_part = [&](uint32_t step, int p) {
         const uint32_t nt = t.nt_begin + step / n_slabs, sb = step % n_slabs;
-        if (!RESIDENT) issue_slab(asrc, sb * kSlab, sa[step & 1u], wave);
-        issue_weights<Frag, MODE>(g, t, nt, sb, sw[WBUF == 2 ? (step & 1u) : 0u], wave, lane);
+        if (!RESIDENT && p < 4) issue_slab_part(asrc, sb * kSlab, sa[step & 1u], wave, p);
+        uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
+#pragma unroll
+        for (uint32_t j = uint32_t(p); j < WC::kPerWave; j += 8u) wc.issue(g, t, nt, sb, wb, wave, j);
     };
     if (RESIDENT)
         for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
-    float4v acc0[4], acc1[4];
+    float4v acc[NF][4];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) { acc0[rb] = float4v{0, 0, 0, 0}; acc1[rb] = float4v{0, 0, 0, 0}; }
-    issue(0);
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < 8; ++p) issue_part(0, p);
     for (uint32_t step = 0; step < n_steps; ++step) {
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
         __syncthreads();                                       // ... from every wave
         const bool more = step + 1 < n_steps;
         const uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
-        Frag c0, c1;
-        c0.template load<FromLds>(wb + staged_row<MODE>(wave, n, 0) * SB, gq);
-        c1.template load<FromLds>(wb + staged_row<MODE>(wave, n, 1) * SB, gq);
+        Frag c[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) c[f].template load<FromLds>(wb + S::image_row(wave, n, f) * SB, gq);
         // A barrier waits for every outstanding load of the wave, so with one weight image
-        // the next step's copies are issued only after the second barrier.
+        // the next step's copies start only after the second barrier.
         if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
-        if (more) issue(step + 1);
-        c0.prepare();
-        c1.prepare();
+#pragma unroll
+        for (int f = 0; f < NF; ++f) c[f].prepare();
         const uint32_t sb = step % n_slabs;
-        slab_mma(sa[RESIDENT ? sb : (step & 1u)], n, gq, c0, c1, acc0, acc1);
+        slab_mma<Frag, NF>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [&](int p) {
+            if (more) issue_part(step + 1, p);
+        });
         if (sb == n_slabs - 1u) {  // column tile complete
             const uint32_t nt = t.nt_begin + step / n_slabs;
-            v2_epilogue<MODE>(g, s_dst, t.a0, t.a1, gq, v2_col<MODE>(nt, wave, n, 0), v2_col<MODE>(nt, wave, n, 1),
-                              acc0, acc1);
+            staged_epilogue<MODE, NF>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
         }
     }
 }
@@ -574,26 +620,27 @@ __global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restr
     if (lane == 0) gl[t] = s;
 }
 
+template <class Frag, int MODE, int NF>
+hipError_t launch_staged(const RoutedGemm& g, hipStream_t s) {
+    const uint32_t n_ntiles = g.n_out / Staged<MODE, NF>::kOut;
+    // About 8 (column tile, slab) steps per workgroup.
+    const uint32_t n_slabs = g.k / kSlab;
+    uint32_t npi = n_slabs >= 8 ? 1u : 8u / n_slabs;
+    if (npi > n_ntiles) npi = n_ntiles;
+    const uint32_t n_chunks = (n_ntiles + npi - 1) / npi;
+    const uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
+    if (n_slabs <= 2)
+        routed_gemm_staged_kernel<Frag, MODE, NF, true><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
+    else
+        routed_gemm_staged_kernel<Frag, MODE, NF, false><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
+    return hipGetLastError();
+}
+
 template <class Frag, int MODE>
 hipError_t launch_routed(const RoutedGemm& g, hipStream_t s) {
-    const uint32_t out_per_v2 = MODE == kGateUp ? kV2Cols / 2 : kV2Cols;
-    if (g.k % kSlab == 0 && g.n_out % out_per_v2 == 0) {
-        const uint32_t n_ntiles = g.n_out / out_per_v2;
-        // About 8 (column tile, slab) steps per workgroup.
-        const uint32_t n_slabs = g.k / kSlab;
-        uint32_t npi = n_slabs >= 8 ? 1u : 8u / n_slabs;
-        if (npi > n_ntiles) npi = n_ntiles;
-        const uint32_t n_chunks = (n_ntiles + npi - 1) / npi;
-        const uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
-        // Two weight images fit beside the activation double buffer unless a slab image is
-        // larger than 40 KB (Q8_0: 68 KB).
-        constexpr int kWBuf = 256 * SlabBytes<Frag>::value <= 40960 ? 2 : 1;
-        if (n_slabs <= 2)
-            routed_gemm_staged_kernel<Frag, MODE, kWBuf, true><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
-        else
-            routed_gemm_staged_kernel<Frag, MODE, kWBuf, false><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
-        return hipGetLastError();
-    }
+    // Two fragments per wave: four (twice the multiplies per activation slab) measured no
+    // faster on gfx950 and needs more than 256 VGPRs for Q4_K/Q2_K.
+    if (g.k % kSlab == 0 && g.n_out % Staged<MODE, 2>::kOut == 0) return launch_staged<Frag, MODE, 2>(g, s);
     const uint32_t n_ntiles = MODE == kGateUp ? g.n_out / 64u : g.n_out / 128u;
     const uint32_t total = g.tile_capacity * n_ntiles;
     const uint32_t blocks = (total + 7u) & ~7u;
