@@ -30,6 +30,21 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def traffic_bytes(config: int, stage: str):
+    """HBM bytes per launch of a stage's routed kernel, from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by what the same
+    counter reads for a plain copy of known size); None when no summary covers it."""
+    path = Path(__file__).resolve().parent / "profiles" / "traffic.json"
+    try:
+        rows = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    for r in rows.get("kernels", []):
+        if r.get("config") == config and r.get("stage") == stage:
+            return int(round((r["fetch_kib"] * rows["fetch_scale"] + r["write_kib"] * rows["write_scale"]) * 1024))
+    return None
+
+
 def calibrate_copy() -> int:
     """A plain device-to-device copy of 512 MiB, 5 times: the reference point that scales
     the FETCH_SIZE / WRITE_SIZE counters (each launch moves 512 MiB in and 512 MiB out)."""
@@ -147,6 +162,20 @@ def main() -> int:
     stage_us = {k: round(v * 1e3, 2) for k, v in stages.items()}
     log(f"stages (us): {stage_us}")
 
+    # Kernel-only durations: each launch of a stage bracketed by HIP events on this stream.
+    def launch_ms(encode, label):
+        vals = []
+        for i in range(reps + 2):
+            s = ctx.segment(); ok, err = encode(s); assert ok, err
+            got = dict(s.commit_timed(sh))
+            if i >= 2:
+                vals.append(got[label])
+        return sum(vals) / len(vals)
+
+    gu_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, gub), "gate/up tiles")
+    dn_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_down(ws.shape, cfg.down_fmt, dnb), "down tiles")
+    log(f"kernels (us): gate/up tiles {gu_kernel_ms * 1e3:.1f}, down tiles {dn_kernel_ms * 1e3:.1f}")
+
     # ---- roofline of the dominant kernel: routed gate/up ----
     plan = ws.plan.tensor.cpu().numpy().view(np.uint32)
     n_groups = int(plan[0])
@@ -154,7 +183,7 @@ def main() -> int:
     dn_row = moe.row_bytes(cfg.down_fmt, I)
     gu_bytes = n_groups * 2 * I * gu_row + N * d * 2 + N * I * 2
     gu_flops = 2.0 * N * 2 * I * d
-    gu_s = stages["gate_up"] / 1e3
+    gu_s = gu_kernel_ms / 1e3
     gu_gbs = gu_bytes / gu_s / 1e9
     gu_tflops = gu_flops / gu_s / 1e12
     dn_bytes = n_groups * d * dn_row + N * I * 2 + N * d * 4
@@ -166,7 +195,9 @@ def main() -> int:
     else:
         roof = {"bound": "mfma", "achieved": round(gu_tflops, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(gu_tflops / F16_MFMA_PEAK_TFLOPS, 4)}
-    roof.update({"kernel": "routed_gemm_kernel<gate/up>", "traffic": None,
+    kernel = f"routed_gemm_staged_kernel<Frag{moe.FORMAT_NAMES[cfg.gate_up_fmt].replace('_', '')}, gate/up>"
+    roof.update({"kernel": kernel, "kernel_us": round(gu_kernel_ms * 1e3, 2),
+                 "traffic": traffic_bytes(args.config, "gate_up"),
                  "algorithmic_bytes": gu_bytes, "algorithmic_flops": gu_flops,
                  "tflops": round(gu_tflops, 1), "gbs": round(gu_gbs, 1)})
     gather_bytes = N * d * 2 + T * d * 2 + N * 4
@@ -176,8 +207,9 @@ def main() -> int:
             "grouping_gather": round(gather_bytes / (stages["grouping_gather"] / 1e3) / 1e9, 1),
             "combine": round(comb_bytes / (stages["combine"] / 1e3) / 1e9, 1),
         },
-        "down": {"us": stage_us["down"], "gbs": round(dn_bytes / (stages["down"] / 1e3) / 1e9, 1),
-                 "tflops": round(2.0 * N * d * I / (stages["down"] / 1e3) / 1e12, 1)},
+        "down": {"kernel_us": round(dn_kernel_ms * 1e3, 2), "gbs": round(dn_bytes / (dn_kernel_ms / 1e3) / 1e9, 1),
+                 "tflops": round(2.0 * N * d * I / (dn_kernel_ms / 1e3) / 1e12, 1),
+                 "traffic": traffic_bytes(args.config, "down")},
         "layer_tflops": round(layer.layer_flops(cfg) * cfg.chunks / (ms_per_step / 1e3) / 1e12, 1),
     }
 
@@ -202,7 +234,7 @@ def main() -> int:
         log(f"cpu baseline {cpu['value']} tokens/s on {threads} threads")
 
     line = {
-        "metric": "MoE-layer prefill tokens/s",
+        "metric": "MoE-layer prefill tokens/s @T=2048/8192; grouped-GEMM % MFMA peak; gather GB/s",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,

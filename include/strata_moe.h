@@ -98,7 +98,7 @@ typedef struct sm_moe_shape {
 #define SM_EXPERT_TILE 64u        /* entries per tile-list tile, prefill_moe.metal:171-173 */
 
 /* Scratch sizes a caller must provide (bytes), given the shape. */
-uint64_t sm_histogram_bytes(const sm_moe_shape* shape); /* ceil(T*k/256) * E * 4     */
+uint64_t sm_histogram_bytes(const sm_moe_shape* shape); /* (ceil(T*k/256) + 1) * E * 4 */
 uint64_t sm_tiles_bytes(const sm_moe_shape* shape);     /* (ceil(T*k/64) + E) * 8    */
 uint64_t sm_format_row_bytes(sm_format fmt, uint64_t values);
 
@@ -113,6 +113,13 @@ sm_status sm_segment_begin(sm_context* ctx, sm_segment** out);
 /* Launches every recorded step in order on `hip_stream` (a hipStream_t; NULL = default
  * stream) and frees the segment. Refused (and the segment freed) if any encode failed. */
 sm_status sm_segment_commit(sm_segment* seg, void* hip_stream);
+/* Measurement form of sm_segment_commit (no counterpart in the reference, whose command
+ * buffers report GPU start/end times instead): brackets every launch with HIP events on
+ * `hip_stream`, waits for the stream, and writes each launch's milliseconds, in recording
+ * order, to ms[0..n) and its static label to labels[i] (labels may be NULL). Refused with
+ * SM_E_ARGUMENT (segment freed, nothing ran) when cap < sm_segment_launches(seg). */
+sm_status sm_segment_commit_timed(sm_segment* seg, void* hip_stream, float* ms, const char** labels, uint32_t cap,
+                                  uint32_t* n_launches);
 /* Discards every recorded step; nothing ran. Frees the segment. */
 void sm_segment_abort(sm_segment* seg);
 /* Message of the first failure recorded in the segment ("" if none). */
@@ -133,7 +140,7 @@ typedef struct sm_route_buffers {
 typedef struct sm_grouping_buffers {
     sm_view ids;              /* I32 [T*k] route ids, token-major                         */
     sm_view mixed_h;          /* F16 [T,d], 16-byte aligned                               */
-    sm_view histogram;        /* U32 [ceil(T*k/256)][E]                                   */
+    sm_view histogram;        /* U32 [ceil(T*k/256) + 1][E]: tile cursors + first slots   */
     sm_view plan;             /* 6400-byte PfPlan slot                                    */
     sm_view tiles;            /* U32x2 [ceil(T*k/64)+E] {group, first_entry}              */
     sm_view source_rows;      /* I32 [T*k]: grouped entry -> token                        */

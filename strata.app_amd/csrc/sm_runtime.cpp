@@ -49,7 +49,7 @@ std::atomic<uint64_t> g_next_handle{1};
 struct sm_segment {
     sm_context* ctx = nullptr;
     // ring_slot >= 0: the step reads that pinned ring slot; an event is recorded after it.
-    struct Step { std::string label; std::function<hipError_t(hipStream_t)> run; int ring_slot = -1; };
+    struct Step { const char* label; std::function<hipError_t(hipStream_t)> run; int ring_slot = -1; };
     std::vector<Step> steps;
     bool failed = false;
     std::string error;
@@ -617,23 +617,67 @@ sm_status sm_segment_begin(sm_context* ctx, sm_segment** out) {
     return SM_OK;
 }
 
-sm_status sm_segment_commit(sm_segment* seg, void* stream) {
-    if (!seg) return SM_E_ARGUMENT;
-    if (seg->failed) { release_ring_slots(seg); delete seg; return SM_E_SEGMENT; }
+namespace {
+
+// Runs the recorded launches in order on `stream`. With `ev` (two events per launch), each
+// launch is bracketed by event records for sm_segment_commit_timed.
+sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
     sm_status st = SM_OK;
     if (!seg->ctx->has_device || hipSetDevice(seg->ctx->device) != hipSuccess) st = SM_E_DEVICE;
-    for (auto& step : seg->steps) {
+    for (size_t i = 0; i < seg->steps.size(); ++i) {
+        auto& step = seg->steps[i];
         if (st != SM_OK) break;
-        if (step.run(reinterpret_cast<hipStream_t>(stream)) != hipSuccess) st = SM_E_DEVICE;
+        if (ev && hipEventRecord(ev[2 * i], stream) != hipSuccess) st = SM_E_DEVICE;
+        if (st == SM_OK && step.run(stream) != hipSuccess) st = SM_E_DEVICE;
+        if (st == SM_OK && ev && hipEventRecord(ev[2 * i + 1], stream) != hipSuccess) st = SM_E_DEVICE;
         if (step.ring_slot >= 0) {
             std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
-            if (hipEventRecord(seg->ctx->ring_ev[step.ring_slot], reinterpret_cast<hipStream_t>(stream)) == hipSuccess)
+            if (hipEventRecord(seg->ctx->ring_ev[step.ring_slot], stream) == hipSuccess)
                 seg->ctx->ring_pending[step.ring_slot] = true;
             else
                 st = SM_E_DEVICE;
         }
     }
     release_ring_slots(seg);
+    return st;
+}
+
+}  // namespace
+
+sm_status sm_segment_commit(sm_segment* seg, void* stream) {
+    if (!seg) return SM_E_ARGUMENT;
+    if (seg->failed) { release_ring_slots(seg); delete seg; return SM_E_SEGMENT; }
+    const sm_status st = run_segment(seg, reinterpret_cast<hipStream_t>(stream), nullptr);
+    delete seg;
+    return st;
+}
+
+sm_status sm_segment_commit_timed(sm_segment* seg, void* stream, float* ms, const char** labels, uint32_t cap,
+                                  uint32_t* n_launches) {
+    if (!seg) return SM_E_ARGUMENT;
+    if (seg->failed || !ms || !n_launches || cap < seg->steps.size()) {
+        const bool failed = seg->failed;
+        release_ring_slots(seg);
+        delete seg;
+        return failed ? SM_E_SEGMENT : SM_E_ARGUMENT;
+    }
+    const size_t n = seg->steps.size();
+    std::vector<hipEvent_t> ev(2 * n, nullptr);
+    sm_status st = SM_OK;
+    if (!seg->ctx->has_device || hipSetDevice(seg->ctx->device) != hipSuccess) st = SM_E_DEVICE;
+    for (size_t i = 0; i < ev.size() && st == SM_OK; ++i)
+        if (hipEventCreate(&ev[i]) != hipSuccess) st = SM_E_DEVICE;
+    const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    if (st == SM_OK) st = run_segment(seg, hs, ev.data());
+    else release_ring_slots(seg);
+    if (st == SM_OK && hipStreamSynchronize(hs) != hipSuccess) st = SM_E_DEVICE;
+    for (size_t i = 0; i < n && st == SM_OK; ++i) {
+        if (hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]) != hipSuccess) st = SM_E_DEVICE;
+        if (labels) labels[i] = seg->steps[i].label;
+    }
+    *n_launches = st == SM_OK ? uint32_t(n) : 0u;
+    for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);  // best effort: nothing to report to the caller
     delete seg;
     return st;
 }

@@ -36,7 +36,7 @@ EXPORTS = (
     "sm_abi_version", "sm_histogram_bytes", "sm_tiles_bytes", "sm_format_row_bytes",
     "sm_context_create", "sm_context_destroy", "sm_buffer_register", "sm_buffer_unregister",
     "sm_segment_begin", "sm_segment_commit", "sm_segment_abort", "sm_segment_error",
-    "sm_segment_launches",
+    "sm_segment_launches", "sm_segment_commit_timed",
     "sm_encode_route", "sm_encode_grouping", "sm_encode_route_gather", "sm_encode_shared_ffn",
     "sm_encode_gate_up", "sm_encode_down", "sm_encode_swiglu", "sm_encode_combine",
     "sm_encode_full_layer", "sm_encode_dequant", "sm_submit_dequant",
@@ -140,6 +140,8 @@ def library() -> C.CDLL:
         "sm_buffer_unregister": (I, [P, U64]),
         "sm_segment_begin": (I, [P, C.POINTER(P)]),
         "sm_segment_commit": (I, [P, P]),
+        "sm_segment_commit_timed": (I, [P, P, C.POINTER(C.c_float), C.POINTER(C.c_char_p), U32,
+                                        C.POINTER(U32)]),
         "sm_segment_abort": (None, [P]),
         "sm_segment_error": (C.c_char_p, [P]),
         "sm_segment_launches": (U32, [P]),
@@ -347,6 +349,19 @@ class Segment:
         self.handle = None
         if st != 0:
             raise RuntimeError(f"sm_segment_commit failed: {STATUS_NAMES.get(st, st)}")
+
+    def commit_timed(self, stream=0):
+        """Commits and returns [(label, milliseconds)] of every launch, in order (waits for
+        the stream)."""
+        n = int(self.lib.sm_segment_launches(self.handle))
+        ms = (C.c_float * max(n, 1))()
+        labels = (C.c_char_p * max(n, 1))()
+        got = C.c_uint32(0)
+        st = self.lib.sm_segment_commit_timed(self.handle, C.c_void_p(stream), ms, labels, max(n, 1), C.byref(got))
+        self.handle = None
+        if st != 0:
+            raise RuntimeError(f"sm_segment_commit_timed failed: {STATUS_NAMES.get(st, st)}")
+        return [(labels[i].decode(), float(ms[i])) for i in range(got.value)]
 
     def abort(self) -> None:
         if self.handle:

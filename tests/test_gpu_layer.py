@@ -93,3 +93,21 @@ def test_layer_config3_zipf_sampled(moe, layer, orc, gpu_ctx, stream):
 def test_layer_config4_chunk_sampled(moe, layer, orc, gpu_ctx, stream):
     print("case layer config 4 chunk 0 (sampled tokens)", flush=True)
     _check_layer(moe, layer, orc, gpu_ctx, stream, layer.CONFIGS[4], n_sample_tokens=24)
+
+
+def test_commit_timed_matches_commit(moe, layer, orc, gpu_ctx, stream):
+    """The measurement commit runs the same launches (same outputs) and reports each one."""
+    print("case timed commit", flush=True)
+    cfg = layer.CONFIGS[0]
+    ws = layer.LayerWorkspace(gpu_ctx, cfg, layer.make_inputs(cfg))
+    ws.run_layer(stream)
+    gub = ws.gate_up_buffers()
+    ref = gu.host(ws.hidden, np.uint16).copy()
+    ws.hidden.tensor.fill_(0x7C01)
+    seg = gpu_ctx.segment()
+    ok, err = seg.encode_prefill_moe_gu(cfg.shape(), cfg.gate_up_fmt, gub)
+    assert ok, err
+    got = seg.commit_timed(stream)
+    assert [label for label, _ in got] == ["gate/up plan validate", "gate/up tiles"]
+    assert all(ms > 0 for _, ms in got)
+    assert np.array_equal(gu.host(ws.hidden, np.uint16), ref)
