@@ -176,7 +176,7 @@ struct FragQ4K {
 // placed under the exponent of 1024 (0x6400 | u = 1024 + u exactly), 1152 is subtracted
 // (exact, giving q), and v_pk_mul_f16 rounds q*d once. A zero code keeps the sign of d.
 __device__ __forceinline__ half2v q80_pair(uint32_t u, uint32_t sel, half2v dd) {
-    const uint32_t biased = __builtin_amdgcn_perm(0u, u, sel) | 0x64006400u;
+    const uint32_t biased = __builtin_amdgcn_perm(0x64646464u, u, sel);  // bytes {u_a, 0x64, u_b, 0x64}
     const half2v q = __builtin_bit_cast(half2v, biased) + half2v{_Float16(-1152.0f), _Float16(-1152.0f)};
     return q * dd;
 }
@@ -200,8 +200,8 @@ struct FragQ80 {
         const uint32_t dw = w[(34 * b) >> 2];
         const _Float16 d = bits_f16(uint16_t(b == 0 ? (dw & 0xffffu) : (dw >> 16)));
         const half2v dd{d, d};
-        const half2v p0 = q80_pair(x0, 0x0c010c00u, dd), p1 = q80_pair(x0, 0x0c030c02u, dd);
-        const half2v p2 = q80_pair(x1, 0x0c010c00u, dd), p3 = q80_pair(x1, 0x0c030c02u, dd);
+        const half2v p0 = q80_pair(x0, 0x04010400u, dd), p1 = q80_pair(x0, 0x04030402u, dd);
+        const half2v p2 = q80_pair(x1, 0x04010400u, dd), p3 = q80_pair(x1, 0x04030402u, dd);
         return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
     }
 };

@@ -11,6 +11,8 @@
 // Routed workgroups walk the grouping's 64-entry tile list; the flat workgroup id is
 // remapped so that consecutive work items (the column tiles of one row tile) land on
 // the same XCD and share its L2.
+#include <type_traits>
+
 #include "sm_device.h"
 #include "sm_launch.h"
 
@@ -250,7 +252,7 @@ __device__ __forceinline__ uint32_t a_pos(uint32_t r, uint32_t c) { return r * 3
 template <int MODE>
 __device__ void zero_cols(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_t c0, uint32_t c1, bool by_dst) {
     const uint32_t width = c1 - c0;
-    for (uint32_t i = threadIdx.x; i < 64u * width; i += kV2Threads) {
+    for (uint32_t i = threadIdx.x; i < 64u * width; i += blockDim.x) {
         const uint32_t r = r0 + i / width, c = c0 + i % width;
         if (r >= r1 || r >= g.n_entries) continue;
         if (MODE == kGateUp) {
@@ -383,7 +385,9 @@ struct Staged {
 // after_s(s) runs after k-step s: the staged kernel issues part s of the next step's copies
 // there, so a wave never blocks on a long burst of memory instructions while it could be
 // multiplying.
-template <class Frag, int NF, class After>
+// Only the first RB 16-row blocks of the tile hold entries (the rest of a 64-row tile past
+// its group's end would multiply padding), so the others are skipped.
+template <class Frag, int NF, int RB, class After>
 __device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag (&c)[NF],
                                          float4v (&acc)[NF][4], After after_s) {
 #pragma unroll
@@ -392,28 +396,24 @@ __device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, con
 #pragma unroll
         for (int f = 0; f < NF; ++f) b[f] = c[f].step(s);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
             const half8 a = *reinterpret_cast<const half8*>(buf + 8u * a_pos(16u * rb + n, 8u * gq + s));
 #pragma unroll
             for (int f = 0; f < NF; ++f) acc[f][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[f], acc[f][rb], 0, 0, 0);
         }
         after_s(s);
-        // Keep each k-step's decode next to its multiplies: hoisting the decodes of later
-        // k-steps ahead would hold NF x 4 decoded registers per k-step at once. The next
-        // k-step's decode still overlaps the multiplies in flight.
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // Writes a finished column tile and clears the accumulators. gate/up: eh[a][col] =
 // half_sat(silu(gate) * up); down: parts[dst[a]][col], with a destination outside [0, N)
 // reported (status bit 1) and the entry's own row zeroed instead.
-template <int MODE, int NF>
+template <int MODE, int NF, int RB>
 __device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint32_t* s_dst, uint32_t a0, uint32_t a1,
                                                 uint32_t col0, int wave, int n, int gq, float4v (&acc)[NF][4]) {
     using S = Staged<MODE, NF>;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t a = a0 + 16u * rb + 4u * gq + i;
@@ -436,7 +436,7 @@ __device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint3
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
+        for (int rb = 0; rb < RB; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
 }
 
 // Bytes moved per lane by one LDS-DMA copy of weight-row slabs: 16 where the slab size
@@ -532,34 +532,44 @@ __global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGe
     };
     if (RESIDENT)
         for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
-    float4v acc[NF][4];
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
 #pragma unroll
     for (int p = 0; p < 8; ++p) issue_part(0, p);
-    for (uint32_t step = 0; step < n_steps; ++step) {
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
-        __syncthreads();                                       // ... from every wave
-        const bool more = step + 1 < n_steps;
-        const uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
-        Frag c[NF];
+    // The step loop, specialised on the number of 16-row blocks holding entries.
+    auto run = [&](auto rb_const) {
+        constexpr int RB = decltype(rb_const)::value;
+        float4v acc[NF][4];
 #pragma unroll
-        for (int f = 0; f < NF; ++f) c[f].template load<FromLds>(wb + S::image_row(wave, n, f) * SB, gq);
-        // A barrier waits for every outstanding load of the wave, so with one weight image
-        // the next step's copies start only after the second barrier.
-        if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
+        for (int f = 0; f < NF; ++f)
 #pragma unroll
-        for (int f = 0; f < NF; ++f) c[f].prepare();
-        const uint32_t sb = step % n_slabs;
-        slab_mma<Frag, NF>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [&](int p) {
-            if (more) issue_part(step + 1, p);
-        });
-        if (sb == n_slabs - 1u) {  // column tile complete
-            const uint32_t nt = t.nt_begin + step / n_slabs;
-            staged_epilogue<MODE, NF>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
+            for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
+        for (uint32_t step = 0; step < n_steps; ++step) {
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
+            __syncthreads();                                       // ... from every wave
+            const bool more = step + 1 < n_steps;
+            const uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
+            Frag c[NF];
+#pragma unroll
+            for (int f = 0; f < NF; ++f) c[f].template load<FromLds>(wb + S::image_row(wave, n, f) * SB, gq);
+            // A barrier waits for every outstanding load of the wave, so with one weight image
+            // the next step's copies start only after the second barrier.
+            if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
+#pragma unroll
+            for (int f = 0; f < NF; ++f) c[f].prepare();
+            const uint32_t sb = step % n_slabs;
+            slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [&](int p) {
+                if (more) issue_part(step + 1, p);
+            });
+            if (sb == n_slabs - 1u) {  // column tile complete
+                const uint32_t nt = t.nt_begin + step / n_slabs;
+                staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
+            }
         }
+    };
+    switch ((t.a1 - t.a0 + 15u) / 16u) {  // workgroup-uniform
+        case 1: run(std::integral_constant<int, 1>()); break;
+        case 2: run(std::integral_constant<int, 2>()); break;
+        case 3: run(std::integral_constant<int, 3>()); break;
+        default: run(std::integral_constant<int, 4>()); break;
     }
 }
 
