@@ -370,10 +370,11 @@ struct Staged {
     static constexpr uint32_t kHalf = 64u * NF;                                // gate/up: gate rows, then up rows
     static constexpr uint32_t kOut = MODE == kGateUp ? 64u * NF : 128u * NF;   // output columns per column tile
     // Column of lane n's fragment f within the column tile (gate/up: the hidden column, the
-    // same for gate fragment f and up fragment f + NF/2).
+    // same for gate fragment f and up fragment f + NF/2). Down interleaves the fragments, so
+    // lane n holds NF adjacent output columns and 16 lanes store whole 128-byte row pieces.
     __device__ static __forceinline__ uint32_t col(int wave, int n, int f) {
         if (MODE == kGateUp) return uint32_t(wave) * (8u * NF) + 16u * uint32_t(f % (NF / 2)) + uint32_t(n);
-        return uint32_t(wave) * (16u * NF) + 16u * uint32_t(f) + uint32_t(n);
+        return uint32_t(wave) * (16u * NF) + NF * uint32_t(n) + uint32_t(f);
     }
     // Row of the packed weight image holding that fragment.
     __device__ static __forceinline__ uint32_t image_row(int wave, int n, int f) {
@@ -382,11 +383,11 @@ struct Staged {
     }
 };
 
-// after_s(s) runs after k-step s: the staged kernel issues part s of the next step's copies
-// there, so a wave never blocks on a long burst of memory instructions while it could be
-// multiplying.
-// Only the first RB 16-row blocks of the tile hold entries (the rest of a 64-row tile past
-// its group's end would multiply padding), so the others are skipped.
+// One 256-value slab of the wave's block. Only the first RB 16-row blocks of the tile hold
+// entries (the rest of a 64-row tile past its group's end would multiply padding), so the
+// others are skipped. after_s(s) runs after k-step s: the staged kernel issues part s of
+// the next step's copies there, so a wave never blocks on a long burst of memory
+// instructions while it could be multiplying.
 template <class Frag, int NF, int RB, class After>
 __device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag (&c)[NF],
                                          float4v (&acc)[NF][4], After after_s) {
@@ -428,9 +429,11 @@ __device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint3
                 const bool good = d < g.n_entries;
                 if (!good) atomicOr(g.status, 2u);
                 const uint64_t row = good ? d : a;
+                typedef float vecf __attribute__((ext_vector_type(NF)));
+                vecf v;
 #pragma unroll
-                for (int f = 0; f < NF; ++f)
-                    g.out_f[row * g.n_out + col0 + S::col(wave, n, f)] = good ? acc[f][rb][i] : 0.0f;
+                for (int f = 0; f < NF; ++f) v[f] = good ? acc[f][rb][i] : 0.0f;
+                *reinterpret_cast<vecf*>(g.out_f + row * g.n_out + col0 + S::col(wave, n, 0)) = v;
             }
         }
 #pragma unroll
@@ -633,9 +636,11 @@ __global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restr
 template <class Frag, int MODE, int NF>
 hipError_t launch_staged(const RoutedGemm& g, hipStream_t s) {
     const uint32_t n_ntiles = g.n_out / Staged<MODE, NF>::kOut;
-    // About 8 (column tile, slab) steps per workgroup.
+    // About 8 (column tile, slab) steps per workgroup; with the activation tile resident
+    // (K <= 512) every column tile of a row tile goes to one workgroup, so the tile is read
+    // once rather than once per workgroup.
     const uint32_t n_slabs = g.k / kSlab;
-    uint32_t npi = n_slabs >= 8 ? 1u : 8u / n_slabs;
+    uint32_t npi = n_slabs <= 2 ? n_ntiles : (n_slabs >= 8 ? 1u : 8u / n_slabs);
     if (npi > n_ntiles) npi = n_ntiles;
     const uint32_t n_chunks = (n_ntiles + npi - 1) / npi;
     const uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
