@@ -13,73 +13,95 @@ constexpr float kWeightFloor = 6.103515625e-5f;  // 2^-14
 // Router GEMM: logits[t,e] = sum_k x[t,k] * W[e,k], F16 activations, F32 weights.
 // Each F32 weight is split into an F16 head and an F16 tail scaled by 2^11
 // (w = hi + lo * 2^-11 to ~2^-24 relative); two MFMA accumulators carry the head and tail
-// products and are merged as fma(lo, 2^-11, hi). Tile: 64 tokens x 64 experts per
-// 256-thread workgroup; wave w owns experts 16w..16w+15 of the tile.
+// products and are merged as fma(lo, 2^-11, hi). Tile: 32 tokens x 64 experts per
+// 256-thread workgroup (two workgroups per CU); wave w owns experts 16w..16w+15. The 32 x
+// 256 activation slab is copied by LDS-DMA into a double-buffered, XOR-swizzled LDS ring;
+// each lane's 64 F32 weights of the next slab are in flight in registers while the current
+// slab is split and multiplied.
 // ---------------------------------------------------------------------------------------
-constexpr int kRouterRows = 64;
+constexpr int kRouterRows = 32;
 constexpr int kRouterCols = 64;
 constexpr int kSlab = 256;
-constexpr int kLdsRow = kSlab + 8;  // halves; padding breaks row-to-bank aliasing
+
+// Position (16-byte chunks) of chunk c of row r in a swizzled rows x 256 slab.
+__device__ __forceinline__ uint32_t slab_pos(uint32_t r, uint32_t c) { return r * 32u + (c ^ (r & 15u)); }
 
 __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
                                                           float* __restrict__ logits,
                                                           uint32_t rows, uint32_t d, uint32_t E) {
-    __shared__ __attribute__((aligned(16))) _Float16 sa[kRouterRows * kLdsRow];
+    __shared__ __attribute__((aligned(1024))) _Float16 sa[2][kRouterRows * kSlab];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const uint32_t t0 = blockIdx.x * kRouterRows;
     const uint32_t e0 = blockIdx.y * kRouterCols;
     const uint32_t e = e0 + 16 * wave + n;
     const bool e_ok = e < E;
-    const float* wrow = w + uint64_t(e_ok ? e : 0) * d;
-    float4v acc_hi[4], acc_lo[4];
+    // Weights of a lane: values 64g .. 64g+63 of each slab of its expert row (row 0 stands in
+    // for experts past E; those outputs are never stored).
+    const float* wrow = w + uint64_t(e_ok ? e : 0) * d + 64 * g;
+    // Activation copy map: wave instruction q = 4*wave + j fills chunk positions
+    // [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk (lane & 31) ^ (R & 15).
+    const _Float16* asrc[4];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
-    for (uint32_t k0 = 0; k0 < d; k0 += kSlab) {
-        // Stage 64 token rows x 256 values of x (16 B per thread per step).
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t R = 2u * (4u * wave + j) + (uint32_t(lane) >> 5);
+        const uint32_t C = (uint32_t(lane) & 31u) ^ (R & 15u);
+        const uint32_t t = t0 + R < rows ? t0 + R : rows - 1u;
+        asrc[j] = x + uint64_t(t) * d + 8u * C;
+    }
+    auto issue_a = [&](uint32_t k0, _Float16* slab) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c >> 5, cc = c & 31;
-            uint32_t t = t0 + r;
-            if (t >= rows) t = rows - 1;
-            const half8 v = *reinterpret_cast<const half8*>(x + uint64_t(t) * d + k0 + 8 * cc);
-            *reinterpret_cast<half8*>(sa + r * kLdsRow + 8 * cc) = v;
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(asrc[j] + k0)),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(slab + (4 * wave + j) * 512)),
+                16, 0, 0);
+    };
+    float4v cw[16], nw[16];
+    auto load_w = [&](uint32_t k0, float4v (&dst)[16]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dst[i] = ld_global<float4v>(wrow + k0 + 4 * i);
+    };
+    float4v acc_hi[2], acc_lo[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
+    const uint32_t n_slabs = d / kSlab;
+    issue_a(0, sa[0]);
+    load_w(0, cw);
+    for (uint32_t sb = 0; sb < n_slabs; ++sb) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this slab's activations and weights
+        __syncthreads();                                       // ... from every wave
+        if (sb + 1 < n_slabs) {
+            issue_a((sb + 1) * kSlab, sa[(sb + 1) & 1u]);
+            load_w((sb + 1) * kSlab, nw);
         }
-        __syncthreads();
+        const _Float16* buf = sa[sb & 1u];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             half8 bh, bl;
-            const int kk = 64 * g + 8 * s;
-            if (e_ok) {
-                const float4v w0 = *reinterpret_cast<const float4v*>(wrow + k0 + kk);
-                const float4v w1 = *reinterpret_cast<const float4v*>(wrow + k0 + kk + 4);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float wf = i < 4 ? w0[i] : w1[i - 4];
-                    const _Float16 h = _Float16(wf);
-                    bh[i] = h;
-                    bl[i] = _Float16((wf - float(h)) * 2048.0f);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) { bh[i] = 0; bl[i] = 0; }
+            for (int i = 0; i < 8; ++i) {
+                const float wf = cw[2 * s + i / 4][i % 4];
+                const _Float16 h = _Float16(wf);
+                bh[i] = h;
+                bl[i] = _Float16((wf - float(h)) * 2048.0f);
             }
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
-                const half8 a = *reinterpret_cast<const half8*>(sa + (16 * rb + n) * kLdsRow + kk);
+            for (int rb = 0; rb < 2; ++rb) {
+                const half8 a = *reinterpret_cast<const half8*>(buf + 8u * slab_pos(16u * rb + n, 8u * g + s));
                 acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_hi[rb], 0, 0, 0);
                 acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_lo[rb], 0, 0, 0);
             }
         }
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cw[i] = nw[i];
     }
     if (!e_ok) return;
     const float b = bias != nullptr ? bias[e] : 0.0f;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t t = t0 + 16 * rb + 4 * g + i;
