@@ -204,7 +204,7 @@ typedef struct sm_shared_buffers {
     sm_view gate_weights;     /* [I_s][d] in the shared format                            */
     sm_view up_weights;       /* [I_s][d]                                                 */
     sm_view down_weights;     /* [d][I_s]                                                 */
-    sm_view gate_vector;      /* [d] sigmoid-gate weights, shared format                  */
+    sm_view gate_vector;      /* [d] sigmoid-gate weights, shared format, 16-byte aligned */
     sm_view hidden;           /* F16 [T,I_s]                                              */
     sm_view output;           /* F32 [T,d]                                                */
     sm_view gate_logit;       /* F32 [T]                                                  */

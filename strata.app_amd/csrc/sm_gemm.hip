@@ -613,8 +613,8 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseGemm g, uint32_t n
         }
 }
 
-// gl[t] = sum_k x[t,k] * gv[k]: one wave per token, lane-strided F32 partial sums reduced
-// by a fixed xor butterfly.
+// gl[t] = sum_k x[t,k] * gv[k]: one wave per token; each lane takes 8 consecutive values
+// per 16-byte load into two F32 partial sums, reduced by a fixed xor butterfly.
 template <bool BF16>
 __global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restrict__ x,
                                                          const uint16_t* __restrict__ gv,
@@ -622,12 +622,20 @@ __global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restr
     const uint32_t t = (blockIdx.x * 256u + threadIdx.x) >> 6;
     const uint32_t lane = threadIdx.x & 63u;
     if (t >= rows) return;
-    float s = 0.0f;
-    for (uint32_t k = lane; k < d; k += 64u) {
-        const uint16_t b = gv[k];
-        const float wv = BF16 ? __builtin_bit_cast(float, uint32_t(b) << 16) : float(bits_f16(b));
-        s = __builtin_fmaf(float(x[uint64_t(t) * d + k]), wv, s);
+    float s0 = 0.0f, s1 = 0.0f;
+    for (uint32_t k = 8u * lane; k < d; k += 512u) {
+        const half8 xv = ld_global<half8>(x + uint64_t(t) * d + k);
+        const u32x4 wv = ld_global<u32x4>(gv + k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t pair = wv[i];
+            const float w0 = BF16 ? __builtin_bit_cast(float, pair << 16) : f16_lo(pair);
+            const float w1 = BF16 ? __builtin_bit_cast(float, pair & 0xffff0000u) : f16_hi(pair);
+            s0 = __builtin_fmaf(float(xv[2 * i]), w0, s0);
+            s1 = __builtin_fmaf(float(xv[2 * i + 1]), w1, s1);
+        }
     }
+    float s = s0 + s1;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s = s + __shfl_xor(s, off);
     if (lane == 0) gl[t] = s;

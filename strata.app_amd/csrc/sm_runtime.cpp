@@ -439,7 +439,7 @@ bool check_shared(Check& c, const sm_moe_shape& s, int fmt, const sm_shared_buff
            c.view(b.gate_weights, w_b, 16, "gate weights", false, r.wg) &&
            c.view(b.up_weights, w_b, 16, "up weights", false, r.wu) &&
            c.view(b.down_weights, w_b, 16, "down weights", false, r.wd) &&
-           c.view(b.gate_vector, uint64_t(s.hidden) * 2, 2, "gate vector", false, r.gv) &&
+           c.view(b.gate_vector, uint64_t(s.hidden) * 2, 16, "gate vector", false, r.gv) &&
            c.view(b.hidden, h_b, 16, "hidden", true, r.hidden) &&
            c.view(b.output, o_b, 16, "output", true, r.out) &&
            c.view(b.gate_logit, uint64_t(s.rows) * 4, 4, "gate logit", true, r.gl);
