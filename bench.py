@@ -59,39 +59,19 @@ def calibrate_copy() -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, help="configuration index (0-4)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="only run a plain 512 MiB device copy (PMC byte-counter calibration)")
-    args = ap.parse_args()
-    if args.calibrate_copy:
-        return calibrate_copy()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
-              f"multi-GPU path — run with --gpus 1", file=sys.stderr)
-        return 2
-
+def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: bool):
+    """Times `steps` full-layer steps of a configuration (after `warmup`), then each stage and
+    the routed kernels on their own. Returns the figures and the host inputs."""
     import numpy as np
     import torch
 
-    import __graft_entry__ as ge
-
-    pkg = ge.load_package()
-    moe, layer = pkg.moe, pkg.layer
-    cfg = layer.CONFIGS[args.config]
+    cfg = layer.CONFIGS[config]
     T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
     N = T * K
-    log(f"config {args.config} ({cfg.name}): generating inputs")
+    log(f"config {config} ({cfg.name}): generating inputs")
     t0 = time.time()
     inp = layer.make_inputs(cfg)
     log(f"inputs ready in {time.time() - t0:.1f}s; uploading")
-    ctx = moe.Context(0)
     chunks = [layer.LayerWorkspace(ctx, cfg, inp, chunk=c) for c in range(cfg.chunks)]
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
@@ -109,31 +89,27 @@ def main() -> int:
             seg.commit(sh)
 
     log("warmup")
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     for ws in chunks:
         st = ws.read_status(sh)
         if st != (0, 0, 0):
             raise RuntimeError(f"layer status {st}")
-    log(f"timing {args.steps} steps")
+    log(f"timing {steps} steps")
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    wall0 = time.perf_counter()
     ev0.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     ev1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
-    tokens_per_step = T * cfg.chunks
-    value = tokens_per_step / (ms_per_step / 1e3)
-    log(f"{ms_per_step:.3f} ms/step, {value:,.0f} tokens/s (wall {wall:.3f}s)")
+    ms_per_step = ev0.elapsed_time(ev1) / steps
+    value = T * cfg.chunks / (ms_per_step / 1e3)
+    log(f"{ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
 
-    # ---- per-stage timing (each stage as its own segment, repeated back to back) ----
     ws = chunks[0]
-    reps = max(5, args.steps)
+    reps = max(5, steps)
 
     def stage_ms(encode):
         for _ in range(2):
@@ -147,21 +123,6 @@ def main() -> int:
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps
 
-    rg, gub, dnb, cob = ws.route_gather_buffers(), ws.gate_up_buffers(), ws.down_buffers(), ws.combine_buffers()
-    shb = ws.shared_buffers()
-    rb, gb = ws.route_buffers(), ws.grouping_buffers()
-    stages = {}
-    stages["route_gather"] = stage_ms(lambda s: s.encode_prefill_moe_full_mode_route_gather(ws.shape, rg))
-    stages["top_k"] = stage_ms(lambda s: s.encode_moe_route(ws.shape, True, rb))
-    stages["grouping_gather"] = stage_ms(lambda s: s.encode_prefill_moe_grouping(ws.shape, gb))
-    if Is:
-        stages["shared_ffn"] = stage_ms(lambda s: s.encode_prefill_moe_shared_ffn(ws.shape, cfg.shared_fmt, shb))
-    stages["gate_up"] = stage_ms(lambda s: s.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, gub))
-    stages["down"] = stage_ms(lambda s: s.encode_prefill_moe_down(ws.shape, cfg.down_fmt, dnb))
-    stages["combine"] = stage_ms(lambda s: s.encode_prefill_moe_combine(ws.shape, cob))
-    stage_us = {k: round(v * 1e3, 2) for k, v in stages.items()}
-    log(f"stages (us): {stage_us}")
-
     # Kernel-only durations: each launch of a stage bracketed by HIP events on this stream.
     def launch_ms(encode, label):
         vals = []
@@ -172,21 +133,76 @@ def main() -> int:
                 vals.append(got[label])
         return sum(vals) / len(vals)
 
+    rg, gub, dnb, cob = ws.route_gather_buffers(), ws.gate_up_buffers(), ws.down_buffers(), ws.combine_buffers()
+    stages = {}
+    if detailed:
+        shb = ws.shared_buffers()
+        rb, gb = ws.route_buffers(), ws.grouping_buffers()
+        stages["route_gather"] = stage_ms(lambda s: s.encode_prefill_moe_full_mode_route_gather(ws.shape, rg))
+        stages["top_k"] = stage_ms(lambda s: s.encode_moe_route(ws.shape, True, rb))
+        stages["grouping_gather"] = stage_ms(lambda s: s.encode_prefill_moe_grouping(ws.shape, gb))
+        if Is:
+            stages["shared_ffn"] = stage_ms(lambda s: s.encode_prefill_moe_shared_ffn(ws.shape, cfg.shared_fmt, shb))
+        stages["gate_up"] = stage_ms(lambda s: s.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, gub))
+        stages["down"] = stage_ms(lambda s: s.encode_prefill_moe_down(ws.shape, cfg.down_fmt, dnb))
+        stages["combine"] = stage_ms(lambda s: s.encode_prefill_moe_combine(ws.shape, cob))
+        log(f"stages (us): { {k: round(v * 1e3, 2) for k, v in stages.items()} }")
     gu_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, gub), "gate/up tiles")
     dn_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_down(ws.shape, cfg.down_fmt, dnb), "down tiles")
     log(f"kernels (us): gate/up tiles {gu_kernel_ms * 1e3:.1f}, down tiles {dn_kernel_ms * 1e3:.1f}")
 
-    # ---- roofline of the dominant kernel: routed gate/up ----
     plan = ws.plan.tensor.cpu().numpy().view(np.uint32)
     n_groups = int(plan[0])
     gu_row = moe.row_bytes(cfg.gate_up_fmt, d)
     dn_row = moe.row_bytes(cfg.down_fmt, I)
-    gu_bytes = n_groups * 2 * I * gu_row + N * d * 2 + N * I * 2
-    gu_flops = 2.0 * N * 2 * I * d
+    return {
+        "cfg": cfg, "inp": inp, "ms_per_step": ms_per_step, "value": value, "stages": stages,
+        "gu_kernel_ms": gu_kernel_ms, "dn_kernel_ms": dn_kernel_ms,
+        "gu_bytes": n_groups * 2 * I * gu_row + N * d * 2 + N * I * 2, "gu_flops": 2.0 * N * 2 * I * d,
+        "dn_bytes": n_groups * d * dn_row + N * I * 2 + N * d * 4, "dn_flops": 2.0 * N * d * I,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, help="configuration index (0-4)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-config3", action="store_true",
+                    help="skip the configuration-3 (T=8192) grouped-GEMM figures")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 512 MiB device copy (PMC byte-counter calibration)")
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
+              f"multi-GPU path — run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch  # noqa: F401  (before the library: one HIP runtime for both)
+
+    import __graft_entry__ as ge
+
+    pkg = ge.load_package()
+    moe, layer = pkg.moe, pkg.layer
+    ctx = moe.Context(0)
+    m = measure(moe, layer, ctx, args.config, args.steps, args.warmup, detailed=True)
+    cfg, inp = m["cfg"], m["inp"]
+    T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
+    N = T * K
+    ms_per_step, value, stages = m["ms_per_step"], m["value"], m["stages"]
+    stage_us = {k: round(v * 1e3, 2) for k, v in stages.items()}
+    gu_kernel_ms, dn_kernel_ms = m["gu_kernel_ms"], m["dn_kernel_ms"]
+
+    # ---- roofline of the dominant kernel: routed gate/up ----
+    gu_bytes, gu_flops, dn_bytes = m["gu_bytes"], m["gu_flops"], m["dn_bytes"]
     gu_s = gu_kernel_ms / 1e3
     gu_gbs = gu_bytes / gu_s / 1e9
     gu_tflops = gu_flops / gu_s / 1e12
-    dn_bytes = n_groups * d * dn_row + N * I * 2 + N * d * 4
     ai = gu_flops / gu_bytes
     bound = "mfma" if ai > F16_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
     if bound == "hbm":
@@ -212,6 +228,21 @@ def main() -> int:
                  "traffic": traffic_bytes(args.config, "down")},
         "layer_tflops": round(layer.layer_flops(cfg) * cfg.chunks / (ms_per_step / 1e3) / 1e12, 1),
     }
+    # ---- the T >= 8192 figures the metric names: configuration 3 (Zipf-skewed) ----
+    if args.config == 2 and not args.no_config3:
+        m3 = measure(moe, layer, ctx, 3, max(3, args.steps // 4), 2, detailed=False)
+        g3 = m3["gu_flops"] / (m3["gu_kernel_ms"] / 1e3) / 1e12
+        d3 = m3["dn_flops"] / (m3["dn_kernel_ms"] / 1e3) / 1e12
+        extra["config3"] = {
+            "workload": "config3:zipf_stress", "tokens": m3["cfg"].rows, "ms_per_step": round(m3["ms_per_step"], 4),
+            "tokens_per_s": round(m3["value"], 1),
+            "gate_up": {"kernel_us": round(m3["gu_kernel_ms"] * 1e3, 2), "tflops": round(g3, 1),
+                        "mfma_frac": round(g3 / F16_MFMA_PEAK_TFLOPS, 4)},
+            "down": {"kernel_us": round(m3["dn_kernel_ms"] * 1e3, 2), "tflops": round(d3, 1),
+                     "mfma_frac": round(d3 / F16_MFMA_PEAK_TFLOPS, 4),
+                     "gbs": round(m3["dn_bytes"] / (m3["dn_kernel_ms"] / 1e3) / 1e9, 1)},
+        }
+        log(f"config 3: {extra['config3']}")
 
     # ---- CPU baseline: the C++ restatement of the same stages on a bounded sample ----
     cpu = None

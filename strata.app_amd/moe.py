@@ -127,6 +127,13 @@ def library() -> C.CDLL:
         return _lib
     if not LIB_PATH.exists():
         raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    # The library and PyTorch must share one HIP runtime. PyTorch carries its own
+    # libamdhip64 under the same soname; loading it first makes this library bind to it,
+    # whereas loading the system runtime first leaves PyTorch without a usable device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(LIB_PATH))
     P, U32, U64, I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
     sig = {
