@@ -40,14 +40,31 @@ hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int
                          const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
 
 // ---- expert stage validation (the reference's plan/destination validators) ----
-// Also copies `snap_words` u64 of the validated expert-address table from `snap_src` (pinned
-// host memory; may be null) into the device snapshot `snap_dst` before validating.
-hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status,
-                                uint32_t n_entries, uint32_t n_experts, uint32_t tile_capacity,
-                                const uint64_t* snap_src, uint64_t* snap_dst, uint32_t snap_words,
-                                hipStream_t s);
+// One plan check for up to two expert stages. The check's verdict goes to `status` and, when
+// set, `status2` (both cleared first). The kernel also copies each stage's validated
+// expert-address table (`snap_words` u64 from pinned host memory `snap_src`, which may be
+// null) into its device snapshot, and zeroes `clear_words` u32 at `clear` (a destination
+// bitset), so a full layer validates its shared plan once for the gate/up and down stages.
+struct PlanCheck {
+    const Plan* plan;
+    const uint32_t* tiles;
+    uint32_t* status;
+    uint32_t* status2;
+    uint32_t n_entries, n_experts, tile_capacity;
+    const uint64_t* snap_src;
+    uint64_t* snap_dst;
+    uint32_t snap_words;
+    const uint64_t* snap_src2;
+    uint64_t* snap_dst2;
+    uint32_t snap_words2;
+    uint32_t* clear;
+    uint32_t clear_words;
+};
+hipError_t launch_plan_validate(const PlanCheck& c, hipStream_t s);
+// Checks that `dst` is a permutation of [0, n_entries) with a bitset (zeroed first unless
+// `bitset_clear` is false because a PlanCheck cleared it).
 hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bitset, uint32_t* status,
-                                       uint32_t n_entries, hipStream_t s);
+                                       uint32_t n_entries, bool bitset_clear, hipStream_t s);
 
 // ---- grouped expert products ----
 struct RoutedGemm {

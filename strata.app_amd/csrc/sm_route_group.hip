@@ -377,27 +377,46 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
 // ---------------------------------------------------------------------------------------
 // The header and per-group checks run one group per thread; the tile-count sum is a block
 // reduction, so the whole plan is checked in a few dependent memory round trips.
-__global__ __launch_bounds__(512) void plan_validate_kernel(const Plan* __restrict__ p,
-                                                            const uint32_t* __restrict__ tiles,
-                                                            uint32_t* __restrict__ status, uint32_t N,
-                                                            uint32_t E, uint32_t cap,
-                                                            const uint64_t* snap_src, uint64_t* snap_dst,
-                                                            uint32_t snap_words) {
+__global__ __launch_bounds__(512) void plan_validate_kernel(PlanCheck c) {
     __shared__ uint32_t s_header_ok, s_groups_ok, s_wave_tiles[8];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    if (snap_src != nullptr)
-        for (uint32_t i = tid; i < snap_words; i += 512u) snap_dst[i] = snap_src[i];
+    for (uint32_t i = blockIdx.x * 512u + tid; i < c.clear_words; i += gridDim.x * 512u) c.clear[i] = 0u;
+    if (blockIdx.x != 0) return;
+    // Address snapshots: every load of a thread is issued before its stores, so the reads
+    // of pinned host memory cost one round trip (tables are at most 3 x 512 words).
+    constexpr int kPer = 3;
+    uint64_t v1[kPer], v2[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + 512u * j;
+        v1[j] = c.snap_src != nullptr && i < c.snap_words ? c.snap_src[i] : 0u;
+        v2[j] = c.snap_src2 != nullptr && i < c.snap_words2 ? c.snap_src2[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + 512u * j;
+        if (c.snap_src != nullptr && i < c.snap_words) c.snap_dst[i] = v1[j];
+        if (c.snap_src2 != nullptr && i < c.snap_words2) c.snap_dst2[i] = v2[j];
+    }
+    const Plan* p = c.plan;
+    const uint32_t N = c.n_entries, E = c.n_experts;
     const uint32_t ng = p->n_groups, nt = p->n_tiles;
+    auto fail = [&]() {
+        atomicOr(c.status, 2u);
+        if (c.status2 != nullptr) atomicOr(c.status2, 2u);
+    };
     if (tid == 0) {
-        *status = 0u;
+        *c.status = 0u;
+        if (c.status2 != nullptr) *c.status2 = 0u;
         s_groups_ok = 1u;
-        s_header_ok = (p->bad == 0u && ng != 0u && ng <= E && ng <= 512u && p->n_entries == N && nt <= cap &&
-                       nt <= p->n_entries && p->grp_start[0] == 0 && p->grp_start[ng] == int32_t(N))
+        s_header_ok = (p->bad == 0u && ng != 0u && ng <= E && ng <= 512u && p->n_entries == N &&
+                       nt <= c.tile_capacity && nt <= p->n_entries && p->grp_start[0] == 0 &&
+                       p->grp_start[ng] == int32_t(N))
                           ? 1u : 0u;
     }
     __syncthreads();
     if (!s_header_ok) {
-        if (tid == 0) atomicOr(status, 2u);
+        if (tid == 0) fail();
         return;
     }
     // Group g: non-empty, inside [0, N), expert in range and strictly ascending.
@@ -416,9 +435,10 @@ __global__ __launch_bounds__(512) void plan_validate_kernel(const Plan* __restri
     uint32_t expected = 0;
     for (uint32_t w = 0; w < 8; ++w) expected += s_wave_tiles[w];
     if (!s_groups_ok || expected != nt) {
-        if (tid == 0) atomicOr(status, 2u);
+        if (tid == 0) fail();
         return;
     }
+    const uint32_t* tiles = c.tiles;
     for (uint32_t i = tid; i < nt; i += 512u) {
         const uint32_t tg = tiles[2 * i], ty = tiles[2 * i + 1];
         bool ok = tg < ng;
@@ -436,7 +456,7 @@ __global__ __launch_bounds__(512) void plan_validate_kernel(const Plan* __restri
             }
             if (i + 1u == nt) ok = ok && tg + 1u == ng && ty + kExpertTile >= end;
         }
-        if (!ok) atomicOr(status, 2u);
+        if (!ok) fail();
     }
 }
 
@@ -499,17 +519,17 @@ hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int
     return hipGetLastError();
 }
 
-hipError_t launch_plan_validate(const Plan* plan, const uint32_t* tiles, uint32_t* status, uint32_t N,
-                                uint32_t E, uint32_t cap, const uint64_t* snap_src, uint64_t* snap_dst,
-                                uint32_t snap_words, hipStream_t s) {
-    plan_validate_kernel<<<1, 512, 0, s>>>(plan, tiles, status, N, E, cap, snap_src, snap_dst, snap_words);
+hipError_t launch_plan_validate(const PlanCheck& c, hipStream_t s) {
+    if (c.snap_words > 1536u || c.snap_words2 > 1536u) return hipErrorInvalidValue;  // E <= 512
+    const uint32_t blocks = 1u + c.clear_words / (512u * 16u);
+    plan_validate_kernel<<<blocks, 512, 0, s>>>(c);
     return hipGetLastError();
 }
 
 hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bits, uint32_t* status, uint32_t N,
-                                       hipStream_t s) {
+                                       bool bitset_clear, hipStream_t s) {
     const uint32_t words = (N + 31) / 32;
-    bitset_clear_kernel<<<(words + 255) / 256, 256, 0, s>>>(bits, words);
+    if (bitset_clear) bitset_clear_kernel<<<(words + 255) / 256, 256, 0, s>>>(bits, words);
     destination_validate_kernel<<<(N + 255) / 256, 256, 0, s>>>(dst, bits, status, N);
     return hipGetLastError();
 }

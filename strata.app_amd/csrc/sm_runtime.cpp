@@ -49,7 +49,11 @@ std::atomic<uint64_t> g_next_handle{1};
 struct sm_segment {
     sm_context* ctx = nullptr;
     // ring_slot >= 0: the step reads that pinned ring slot; an event is recorded after it.
-    struct Step { const char* label; std::function<hipError_t(hipStream_t)> run; int ring_slot = -1; };
+    struct Step {
+        const char* label;
+        std::function<hipError_t(hipStream_t)> run;
+        int ring_slot = -1, ring_slot2 = -1;
+    };
     std::vector<Step> steps;
     bool failed = false;
     std::string error;
@@ -317,7 +321,8 @@ int claim_ring_slot(sm_context* ctx, const std::vector<uint64_t>& table) {
 void release_ring_slots(sm_segment* seg) {
     std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
     for (const auto& step : seg->steps)
-        if (step.ring_slot >= 0) seg->ctx->ring_claimed[step.ring_slot] = false;
+        for (const int slot : {step.ring_slot, step.ring_slot2})
+            if (slot >= 0) seg->ctx->ring_claimed[slot] = false;
 }
 
 struct GateUpRes { WeightsRes w; uintptr_t xs, plan, tiles, hidden, status; };
@@ -338,15 +343,8 @@ bool check_gate_up(Check& c, const sm_moe_shape& s, int fmt, const sm_gate_up_bu
            c.view(b.status, 4, 4, "status", true, r.status);
 }
 
-sm_status encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r) {
-    const int slot = claim_ring_slot(seg->ctx, r.w.table);
-    if (slot == -2) return SM_E_SEGMENT;
-    if (slot == -3) return SM_E_DEVICE;
-    const uint64_t* snap_src = slot >= 0 ? seg->ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
-    uint64_t* snap_dst = reinterpret_cast<uint64_t*>(r.w.snapshot);
-    const uint32_t words = uint32_t(r.w.table.size());
+sm::RoutedGemm gate_up_gemm(const sm_moe_shape& s, int fmt, const GateUpRes& r) {
     const uint32_t N = s.rows * s.top_k;
-    const uint32_t cap = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
     sm::RoutedGemm g{};
     g.addresses = reinterpret_cast<const uint64_t*>(r.w.snapshot);
     g.a = reinterpret_cast<const _Float16*>(r.xs);
@@ -356,14 +354,36 @@ sm_status encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt,
     g.status = reinterpret_cast<uint32_t*>(r.status);
     g.n_entries = N;
     g.n_experts = s.n_experts;
-    g.tile_capacity = cap;
+    g.tile_capacity = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
     g.k = s.hidden;
     g.n_out = s.expert_ff;
     g.row_bytes = fmt_row_bytes(fmt, s.hidden);
-    const uint32_t E = s.n_experts;
-    add_step(seg, "gate/up plan validate", [=](hipStream_t st) {
-        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, snap_src, snap_dst, words, st);
-    });
+    return g;
+}
+
+// Plan check of one stage, with its snapshot copy from ring slot `slot` (-1: none).
+sm::PlanCheck stage_check(sm_context* ctx, const sm::RoutedGemm& g, int slot, uintptr_t snapshot, uint32_t words) {
+    sm::PlanCheck c{};
+    c.plan = g.plan;
+    c.tiles = g.tiles;
+    c.status = g.status;
+    c.n_entries = g.n_entries;
+    c.n_experts = g.n_experts;
+    c.tile_capacity = g.tile_capacity;
+    c.snap_src = slot >= 0 ? ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
+    c.snap_dst = reinterpret_cast<uint64_t*>(snapshot);
+    c.snap_words = words;
+    return c;
+}
+
+sm_status claim_status(int slot) { return slot == -2 ? SM_E_SEGMENT : slot == -3 ? SM_E_DEVICE : SM_OK; }
+
+sm_status encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r) {
+    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+    if (claim_status(slot) != SM_OK) return claim_status(slot);
+    const sm::RoutedGemm g = gate_up_gemm(s, fmt, r);
+    const sm::PlanCheck c = stage_check(seg->ctx, g, slot, r.w.snapshot, uint32_t(r.w.table.size()));
+    add_step(seg, "gate/up plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
     seg->steps.back().ring_slot = slot;
     add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fmt), g, st); });
     return SM_OK;
@@ -388,15 +408,8 @@ bool check_down(Check& c, const sm_moe_shape& s, int fmt, const sm_down_buffers&
            c.view(b.status, 4, 4, "status", true, r.status);
 }
 
-sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r) {
-    const int slot = claim_ring_slot(seg->ctx, r.w.table);
-    if (slot == -2) return SM_E_SEGMENT;
-    if (slot == -3) return SM_E_DEVICE;
-    const uint64_t* snap_src = slot >= 0 ? seg->ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
-    uint64_t* snap_dst = reinterpret_cast<uint64_t*>(r.w.snapshot);
-    const uint32_t words = uint32_t(r.w.table.size());
+sm::RoutedGemm down_gemm(const sm_moe_shape& s, int fmt, const DownRes& r) {
     const uint32_t N = s.rows * s.top_k;
-    const uint32_t cap = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
     sm::RoutedGemm g{};
     g.addresses = reinterpret_cast<const uint64_t*>(r.w.snapshot);
     g.a = reinterpret_cast<const _Float16*>(r.hidden);
@@ -407,21 +420,68 @@ sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, co
     g.status = reinterpret_cast<uint32_t*>(r.status);
     g.n_entries = N;
     g.n_experts = s.n_experts;
-    g.tile_capacity = cap;
+    g.tile_capacity = uint32_t(ceil_div(N, SM_EXPERT_TILE) + s.n_experts);
     g.k = s.expert_ff;
     g.n_out = s.hidden;
     g.row_bytes = fmt_row_bytes(fmt, s.expert_ff);
-    const uint32_t E = s.n_experts;
-    add_step(seg, "down plan validate", [=](hipStream_t st) {
-        return sm::launch_plan_validate(g.plan, g.tiles, g.status, N, E, cap, snap_src, snap_dst, words, st);
-    });
-    seg->steps.back().ring_slot = slot;
-    // The destination bitset borrows the head of `parts`, which the down tiles overwrite
-    // (the reference's prefill_moe_down_dispatch.mm:470-520 does the same).
+    return g;
+}
+
+// The destination bitset borrows the head of `parts`, which the down tiles overwrite
+// (the reference's prefill_moe_down_dispatch.mm:470-520 does the same).
+void add_down_tail(sm_segment* seg, int fmt, const sm::RoutedGemm& g, bool bitset_clear) {
     add_step(seg, "down destination validate", [=](hipStream_t st) {
-        return sm::launch_destination_validate(g.dst, reinterpret_cast<uint32_t*>(g.out_f), g.status, N, st);
+        return sm::launch_destination_validate(g.dst, reinterpret_cast<uint32_t*>(g.out_f), g.status, g.n_entries,
+                                               bitset_clear, st);
     });
     add_step(seg, "down tiles", [=](hipStream_t st) { return sm::launch_down(Fmt(fmt), g, st); });
+}
+
+sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r) {
+    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+    if (claim_status(slot) != SM_OK) return claim_status(slot);
+    const sm::RoutedGemm g = down_gemm(s, fmt, r);
+    const sm::PlanCheck c = stage_check(seg->ctx, g, slot, r.w.snapshot, uint32_t(r.w.table.size()));
+    add_step(seg, "down plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
+    seg->steps.back().ring_slot = slot;
+    add_down_tail(seg, fmt, g, true);
+    return SM_OK;
+}
+
+// Full layer, both expert stages on one plan and tile list: the plan is checked once, for
+// both status words, and the same launch copies both address snapshots and clears the
+// destination bitset. Stages with distinct plan or tile views are encoded separately.
+sm_status encode_experts_launch(sm_segment* seg, const sm_moe_shape& s, int fmt_gu, const GateUpRes& gu, int fmt_dn,
+                                const DownRes& dn) {
+    if (gu.plan != dn.plan || gu.tiles != dn.tiles) {
+        sm_status st = encode_gate_up_launch(seg, s, fmt_gu, gu);
+        return st != SM_OK ? st : encode_down_launch(seg, s, fmt_dn, dn);
+    }
+    const int slot1 = claim_ring_slot(seg->ctx, gu.w.table);
+    if (claim_status(slot1) != SM_OK) return claim_status(slot1);
+    const int slot2 = claim_ring_slot(seg->ctx, dn.w.table);
+    if (claim_status(slot2) != SM_OK) {
+        if (slot1 >= 0) {
+            std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
+            seg->ctx->ring_claimed[slot1] = false;
+        }
+        return claim_status(slot2);
+    }
+    const sm::RoutedGemm g = gate_up_gemm(s, fmt_gu, gu);
+    const sm::RoutedGemm d = down_gemm(s, fmt_dn, dn);
+    sm::PlanCheck c = stage_check(seg->ctx, g, slot1, gu.w.snapshot, uint32_t(gu.w.table.size()));
+    const sm::PlanCheck c2 = stage_check(seg->ctx, d, slot2, dn.w.snapshot, uint32_t(dn.w.table.size()));
+    c.status2 = d.status;
+    c.snap_src2 = c2.snap_src;
+    c.snap_dst2 = c2.snap_dst;
+    c.snap_words2 = c2.snap_words;
+    c.clear = reinterpret_cast<uint32_t*>(d.out_f);
+    c.clear_words = uint32_t(ceil_div(d.n_entries, 32));
+    add_step(seg, "expert plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
+    seg->steps.back().ring_slot = slot1;
+    seg->steps.back().ring_slot2 = slot2;
+    add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fmt_gu), g, st); });
+    add_down_tail(seg, fmt_dn, d, false);
     return SM_OK;
 }
 
@@ -630,10 +690,11 @@ sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
         if (ev && hipEventRecord(ev[2 * i], stream) != hipSuccess) st = SM_E_DEVICE;
         if (st == SM_OK && step.run(stream) != hipSuccess) st = SM_E_DEVICE;
         if (st == SM_OK && ev && hipEventRecord(ev[2 * i + 1], stream) != hipSuccess) st = SM_E_DEVICE;
-        if (step.ring_slot >= 0) {
+        for (const int slot : {step.ring_slot, step.ring_slot2}) {
+            if (slot < 0) continue;
             std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
-            if (hipEventRecord(seg->ctx->ring_ev[step.ring_slot], stream) == hipSuccess)
-                seg->ctx->ring_pending[step.ring_slot] = true;
+            if (hipEventRecord(seg->ctx->ring_ev[slot], stream) == hipSuccess)
+                seg->ctx->ring_pending[slot] = true;
             else
                 st = SM_E_DEVICE;
         }
@@ -926,8 +987,7 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
         }
     encode_route_gather_launch(seg, s, rr, ro, gr);
     if (has_shared) encode_shared_launch(seg, s, f->shared, sr);
-    if ((st = encode_gate_up_launch(seg, s, f->gate_up, gu)) != SM_OK) return ring_fail(seg, st);
-    if ((st = encode_down_launch(seg, s, f->down, dn)) != SM_OK) return ring_fail(seg, st);
+    if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
     encode_combine_launch(seg, s, co);
     return SM_OK;
 }

@@ -110,3 +110,29 @@ def test_swiglu_and_combine_bit_exact(moe, orc, gpu_ctx, stream):
     gu.run(gpu_ctx, stream, lambda s: s.encode_prefill_moe_combine(shape0, cb0))
     ref0 = orc.combine(parts, w, None, None, T, K, d)
     assert np.array_equal(gu.host(bo, np.float32).reshape(T, d).view(np.uint32), ref0.view(np.uint32))
+
+
+def test_full_layer_clears_both_status_words_and_reports_null_address(moe, layer, orc, gpu_ctx, stream):
+    """The full layer checks its plan once for both expert stages: both status words start
+    cleared, and a missing weight address is still reported by the gate/up tiles."""
+    print("case failure full layer status words", flush=True)
+    cfg, inp, ws = _small_layer(moe, layer, gpu_ctx)
+    ws.status.tensor.fill_(-1)                       # stale bits from an earlier failure
+    ws.run_layer(stream)
+    assert ws.read_status(stream) == (0, 0, 0)
+    E = cfg.n_experts
+    ids = gu.host(ws.ids, np.int32)
+    victim = int(np.bincount(ids, minlength=E).argmax())
+    addr = list(ws.addresses)
+    addr[3 * victim + 1] = 0
+    table = moe.ExpertTable(addr, ws.snap_gu.view(), [ws.w_gate.view(), ws.w_up.view()])
+    lb = ws.layer_buffers()
+    lb.gate_up = moe.GateUpBuffers(table.struct, ws.xs.view(), ws.plan.view(), ws.tiles.view(), ws.hidden.view(),
+                                   ws.status.view(0, 4))
+    ws.status.tensor.fill_(-1)
+    seg = gpu_ctx.segment()
+    ok, err = seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, lb, keep=table)
+    assert ok, err
+    seg.commit(stream)
+    bad, st_gu, st_dn = ws.read_status(stream)
+    assert (bad, st_gu, st_dn) == (0, 1, 0)
