@@ -38,9 +38,10 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
     const uint32_t e0 = blockIdx.y * kRouterCols;
     const uint32_t e = e0 + 16 * wave + n;
     const bool e_ok = e < E;
-    // Weights of a lane: values 64g .. 64g+63 of each slab of its expert row (row 0 stands in
-    // for experts past E; those outputs are never stored).
-    const float* wrow = w + uint64_t(e_ok ? e : 0) * d + 64 * g;
+    // K mapping: k-step s feeds lane group g the values 32s + 8g .. 32s + 8g + 7 of a slab,
+    // so the four lane groups of an expert row read one contiguous 128-byte piece per
+    // k-step (row 0 stands in for experts past E; those outputs are never stored).
+    const float* wrow = w + uint64_t(e_ok ? e : 0) * d + 8 * g;
     // Activation copy map: wave instruction q = 4*wave + j fills chunk positions
     // [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk (lane & 31) ^ (R & 15).
     const _Float16* asrc[4];
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
     float4v cw[16], nw[16];
     auto load_w = [&](uint32_t k0, float4v (&dst)[16]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dst[i] = ld_global<float4v>(wrow + k0 + 4 * i);
+        for (int i = 0; i < 16; ++i) dst[i] = ld_global<float4v>(wrow + k0 + 32 * (i >> 1) + 4 * (i & 1));
     };
     float4v acc_hi[2], acc_lo[2];
 #pragma unroll
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
             }
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
-                const half8 a = *reinterpret_cast<const half8*>(buf + 8u * slab_pos(16u * rb + n, 8u * g + s));
+                const half8 a = *reinterpret_cast<const half8*>(buf + 8u * slab_pos(16u * rb + n, 4u * s + g));
                 acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_hi[rb], 0, 0, 0);
                 acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_lo[rb], 0, 0, 0);
             }
@@ -338,9 +339,11 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(const int32_t* __res
     dst[slot] = int32_t(entry);
 }
 
-// Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count; 16 bytes per thread,
-// 4 independent copies in flight per thread. The plan header is checked first as in the
+// Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. A workgroup copies kGatherRows
+// grouped rows; a row's source index is workgroup-uniform, and each thread issues its loads
+// for all rows before its stores (16 bytes each). The plan header is checked first as in the
 // reference's gather (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
+constexpr uint32_t kGatherRows = 8;
 __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t rows,
                                                      uint32_t vpr, const int32_t* __restrict__ src,
                                                      const Plan* __restrict__ plan, uint32_t N,
@@ -349,26 +352,20 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
     if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) return;
     const int32_t sorted_signed = plan->grp_start[ng];
     if (sorted_signed < 0 || uint32_t(sorted_signed) != N - plan->bad) return;
-    const uint64_t total = uint64_t(uint32_t(sorted_signed)) * vpr;
-    const uint64_t base = uint64_t(blockIdx.x) * 1024u + threadIdx.x;
-    u32x4 v[4];
-    uint64_t out[4];
-    bool ok[4];
+    const uint32_t sorted = uint32_t(sorted_signed);
+    const uint32_t a0 = blockIdx.x * kGatherRows;
+    int32_t s[kGatherRows];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint64_t idx = base + 256u * j;
-        ok[j] = idx < total;
-        out[j] = idx;
-        if (ok[j]) {
-            const uint64_t a = idx / vpr, c = idx % vpr;
-            const int32_t s = src[a];
-            ok[j] = s >= 0 && uint32_t(s) < rows;
-            if (ok[j]) v[j] = x[uint64_t(s) * vpr + c];
-        }
+    for (uint32_t r = 0; r < kGatherRows; ++r) s[r] = a0 + r < sorted ? src[a0 + r] : -1;
+    for (uint32_t c = threadIdx.x; c < vpr; c += 256u) {
+        u32x4 v[kGatherRows];
+#pragma unroll
+        for (uint32_t r = 0; r < kGatherRows; ++r)
+            if (s[r] >= 0 && uint32_t(s[r]) < rows) v[r] = x[uint64_t(uint32_t(s[r])) * vpr + c];
+#pragma unroll
+        for (uint32_t r = 0; r < kGatherRows; ++r)
+            if (s[r] >= 0 && uint32_t(s[r]) < rows) xs[uint64_t(a0 + r) * vpr + c] = v[r];
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (ok[j]) xs[out[j]] = v[j];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -512,8 +509,7 @@ hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32
 hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
                          const Plan* plan, uint32_t N, _Float16* xs, hipStream_t s) {
     const uint32_t vpr = d / 8;
-    const uint64_t total = uint64_t(N) * vpr;
-    const uint32_t blocks = uint32_t((total + 1023) / 1024);
+    const uint32_t blocks = (N + kGatherRows - 1) / kGatherRows;
     gather_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
                                          reinterpret_cast<u32x4*>(xs));
     return hipGetLastError();
