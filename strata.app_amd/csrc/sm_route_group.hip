@@ -341,9 +341,10 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(const int32_t* __res
 
 // Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. A workgroup copies kGatherRows
 // grouped rows; a row's source index is workgroup-uniform, and each thread issues its loads
-// for all rows before its stores (16 bytes each). The plan header is checked first as in the
-// reference's gather (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
-constexpr uint32_t kGatherRows = 8;
+// for all rows before its stores (16 bytes each). The stores are non-temporal: the grouped rows
+// are a write-once stream. The plan header is checked first as in the reference's gather
+// (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
+constexpr uint32_t kGatherRows = 4;
 __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t rows,
                                                      uint32_t vpr, const int32_t* __restrict__ src,
                                                      const Plan* __restrict__ plan, uint32_t N,
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
             if (s[r] >= 0 && uint32_t(s[r]) < rows) v[r] = x[uint64_t(uint32_t(s[r])) * vpr + c];
 #pragma unroll
         for (uint32_t r = 0; r < kGatherRows; ++r)
-            if (s[r] >= 0 && uint32_t(s[r]) < rows) xs[uint64_t(a0 + r) * vpr + c] = v[r];
+            if (s[r] >= 0 && uint32_t(s[r]) < rows) __builtin_nontemporal_store(v[r], &xs[uint64_t(a0 + r) * vpr + c]);
     }
 }
 
