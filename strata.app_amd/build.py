@@ -18,7 +18,7 @@ BUILD = HERE / "_build"
 LIB = HERE / "libstrata_moe.so"
 INCLUDE = HERE.parent / "include"
 
-HIP_SOURCES = ["sm_route_group.hip", "sm_gemm.hip", "sm_post.hip", "sm_runtime.cpp"]
+HIP_SOURCES = ["sm_route_group.hip", "sm_gemm.hip", "sm_wide.hip", "sm_post.hip", "sm_runtime.cpp"]
 HOST_SOURCES = ["sm_synth.cpp"]
 
 HIPCC_FLAGS = [

@@ -181,6 +181,7 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
         zero_tile<MODE>(g, tile_index * 64u, tile_index * 64u + 64u, nt);
         return;
     }
+    if (gend - gfirst >= g.wide_min) return;  // the wide kernel's group
     const uint32_t a1 = a0 + 64u < gend ? a0 + 64u : gend;
     const uint64_t* addr = g.addresses + 3u * uint32_t(ex);
     const uint8_t* w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
@@ -275,56 +276,63 @@ struct TileWork {
     const uint8_t* w1;
 };
 
-// Shared prologue of the staged kernels: reads the status word and the plan's tile count once,
-// maps the workgroup to its item over the real tiles (XCD-aware), and validates the tile
-// against the plan. Returns false when the workgroup has nothing (more) to do; failed
-// tiles have written their zeros and status bits by then. Every thread of the workgroup
-// takes the same branch.
-template <int MODE>
-__device__ bool v2_prologue(const RoutedGemm& g, uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks,
-                            uint32_t out_per_nt, TileWork& t) {
-    __shared__ uint32_t s_flag, s_tiles;
+// Tile enumeration of the persistent staged kernels (512 threads), once per workgroup:
+// reads the status word and counts, per plan group below wide_min entries, its
+// ceil(size / 64) tiles; s_pref[gi] = tiles of the groups before gi. The plan has been
+// checked against the tile list by the plan validator, so these are exactly the list's
+// tiles of those groups, in order. A group that fails the range checks contributes no
+// tiles and reports status bit 1 (it cannot occur behind a passed plan check). Returns the
+// status word read at start.
+__device__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag) {
     const Plan* p = g.plan;
-    if (threadIdx.x == 0) {
-        s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_tiles = p->n_tiles;
-    }
-    __syncthreads();
-    if (s_flag & 2u) {  // invalid plan or permutation: every tile slot writes zeros
-        if (blockIdx.x >= g.tile_capacity * n_chunks) return false;
-        const uint32_t ti = blockIdx.x / n_chunks, ch = blockIdx.x % n_chunks;
-        const uint32_t nb = ch * npi, ne = nb + npi < n_ntiles ? nb + npi : n_ntiles;
-        zero_cols<MODE>(g, ti * 64u, ti * 64u + 64u, nb * out_per_nt, ne * out_per_nt, false);
-        return false;
-    }
-    const uint32_t real = (s_tiles < g.tile_capacity ? s_tiles : g.tile_capacity) * n_chunks;
-    const uint32_t w = xcd_remap(blockIdx.x, real);
-    if (w >= real) return false;
-    const uint32_t tile_index = w / n_chunks, chunk = w % n_chunks;
-    t.nt_begin = chunk * npi;
-    t.nt_end = t.nt_begin + npi < n_ntiles ? t.nt_begin + npi : n_ntiles;
-    const uint32_t tg = g.tiles[2 * tile_index], a0 = g.tiles[2 * tile_index + 1];
-    bool ok = tg < p->n_groups;
-    uint32_t gend = 0;
-    int32_t ex = -1;
-    if (ok) {
-        const int32_t f = p->grp_start[tg], e = p->grp_start[tg + 1];
-        ex = p->grp_e[tg];
-        ok = f >= 0 && e > f && uint32_t(e) <= p->n_entries && ex >= 0 && uint32_t(ex) < g.n_experts;
-        if (ok) {
-            gend = uint32_t(e);
-            ok = a0 >= uint32_t(f) && a0 < gend && (a0 - uint32_t(f)) % 64u == 0u;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t ng = p->n_groups < 512u ? p->n_groups : 512u;
+    uint32_t n = 0;
+    if (tid < ng) {
+        const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
+        if (f >= 0 && e > f && uint32_t(e) <= g.n_entries && ex >= 0 && uint32_t(ex) < g.n_experts) {
+            if (uint32_t(e - f) < g.wide_min) n = (uint32_t(e - f) + 63u) / 64u;
+        } else {
+            atomicOr(g.status, 2u);
         }
     }
-    if (!ok) {
-        if (threadIdx.x == 0) atomicOr(g.status, 2u);
-        zero_cols<MODE>(g, tile_index * 64u, tile_index * 64u + 64u, t.nt_begin * out_per_nt,
-                        t.nt_end * out_per_nt, false);
-        return false;
+#pragma unroll
+    for (uint32_t off = 1; off < 64u; off <<= 1) {
+        const uint32_t y = __shfl_up(n, off);
+        if (lane >= off) n += y;
     }
-    t.a0 = a0;
-    t.a1 = a0 + 64u < gend ? a0 + 64u : gend;
-    const uint64_t* addr = g.addresses + 3u * uint32_t(ex);
+    if (lane == 63u) s_wsum[wave] = n;
+    __syncthreads();
+    uint32_t base = 0;
+    for (uint32_t w = 0; w < wave; ++w) base += s_wsum[w];
+    s_pref[tid + 1] = base + n;
+    if (tid == 0) s_pref[0] = 0;
+    __syncthreads();
+    return *s_flag;
+}
+
+// Item `item` (tile k = item / n_chunks of the enumeration, column chunk item % n_chunks):
+// its rows, column tiles and weights. Returns false when the item is done already: an
+// expert without weights has zeroed its rows and set status bit 0. Uniform per workgroup.
+template <int MODE>
+__device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item, uint32_t n_ntiles,
+                            uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t) {
+    const Plan* p = g.plan;
+    const uint32_t k = item / n_chunks, chunk = item - k * n_chunks;
+    uint32_t lo = 0, hi = 512;
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (s_pref[mid] <= k) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t f = uint32_t(p->grp_start[lo]), e = uint32_t(p->grp_start[lo + 1]);
+    const uint32_t ex = uint32_t(p->grp_e[lo]);
+    t.nt_begin = chunk * npi;
+    t.nt_end = t.nt_begin + npi < n_ntiles ? t.nt_begin + npi : n_ntiles;
+    t.a0 = f + 64u * (k - s_pref[lo]);
+    t.a1 = t.a0 + 64u < e ? t.a0 + 64u : e;
+    const uint64_t* addr = g.addresses + 3u * ex;
     t.w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
     t.w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
     if (t.w0 == nullptr || t.w1 == nullptr) {
@@ -512,8 +520,25 @@ __global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGe
     __shared__ __attribute__((aligned(1024))) _Float16 sa[2][64 * kSlab];
     __shared__ __attribute__((aligned(1024))) uint8_t sw[WBUF][StagedBuffers<Frag, NF>::kImage];
     __shared__ uint32_t s_dst[64];  // down: destination row of each tile row
+    __shared__ uint32_t s_pref[513], s_wsum[8], s_flag;
+    const uint32_t flag = scan_small_tiles(g, s_pref, s_wsum, &s_flag);
+    if (flag & 2u) {  // invalid plan or permutation: every tile slot writes zeros
+        for (uint32_t slot = blockIdx.x; slot < g.tile_capacity * n_chunks; slot += gridDim.x) {
+            const uint32_t ti = slot / n_chunks, ch = slot % n_chunks;
+            const uint32_t nb = ch * npi, ne = nb + npi < n_ntiles ? nb + npi : n_ntiles;
+            zero_cols<MODE>(g, ti * 64u, ti * 64u + 64u, nb * S::kOut, ne * S::kOut, false);
+        }
+        return;
+    }
+    // Persistent: XCD x (workgroups b with b % 8 == x) takes the contiguous item range
+    // [x * per, (x + 1) * per), so the column chunks of a tile share that XCD's L2.
+    const uint32_t items = s_pref[512] * n_chunks;
+    const uint32_t per = (items + 7u) >> 3, x = blockIdx.x & 7u, P = gridDim.x >> 3;
+    const uint32_t i_end = (x + 1u) * per < items ? (x + 1u) * per : items;
+    for (uint32_t item = x * per + (blockIdx.x >> 3); item < i_end; item += P) {
+    __syncthreads();  // the previous item's reads of LDS are done
     TileWork t;
-    if (!v2_prologue<MODE>(g, n_ntiles, npi, n_chunks, S::kOut, t)) return;
+    if (!staged_item<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, S::kOut, t)) continue;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, gq = lane >> 4;
     // Read once here rather than in each epilogue, where a dependent global load would also
     // wait for the copies of the next step (visible after the first loop barrier).
@@ -573,6 +598,7 @@ __global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGe
         case 2: run(std::integral_constant<int, 2>()); break;
         case 3: run(std::integral_constant<int, 3>()); break;
         default: run(std::integral_constant<int, 4>()); break;
+    }
     }
 }
 
@@ -641,6 +667,20 @@ __global__ __launch_bounds__(256) void gate_logit_kernel(const _Float16* __restr
     if (lane == 0) gl[t] = s;
 }
 
+// Compute units of the current device (queried once; 256 if the query fails).
+uint32_t device_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cus = v;
+        else
+            cus = 256;
+    }
+    return uint32_t(cus);
+}
+
 template <class Frag, int MODE, int NF>
 hipError_t launch_staged(const RoutedGemm& g, hipStream_t s) {
     const uint32_t n_ntiles = g.n_out / Staged<MODE, NF>::kOut;
@@ -651,7 +691,12 @@ hipError_t launch_staged(const RoutedGemm& g, hipStream_t s) {
     uint32_t npi = n_slabs <= 2 ? n_ntiles : (n_slabs >= 8 ? 1u : 8u / n_slabs);
     if (npi > n_ntiles) npi = n_ntiles;
     const uint32_t n_chunks = (n_ntiles + npi - 1) / npi;
-    const uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
+    // Persistent: one workgroup per CU (each holds about 130 KB of LDS), never more than the
+    // tile slots, in whole groups of 8 (one per XCD).
+    uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
+    const uint32_t cap = device_cus() & ~7u;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 8u) blocks = 8u;
     if (n_slabs <= 2)
         routed_gemm_staged_kernel<Frag, MODE, NF, true><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
     else
@@ -660,7 +705,11 @@ hipError_t launch_staged(const RoutedGemm& g, hipStream_t s) {
 }
 
 template <class Frag, int MODE>
-hipError_t launch_routed(const RoutedGemm& g, hipStream_t s) {
+hipError_t launch_routed(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
+    if (g.wide_min != ~0u) {
+        const hipError_t e = launch_wide(fmt, MODE == kGateUp, g, s);
+        if (e != hipSuccess) return e;
+    }
     // Two fragments per wave: four (twice the multiplies per activation slab) measured no
     // faster on gfx950 and needs more than 256 VGPRs for Q4_K/Q2_K.
     if (g.k % kSlab == 0 && g.n_out % Staged<MODE, 2>::kOut == 0) return launch_staged<Frag, MODE, 2>(g, s);
@@ -685,18 +734,18 @@ hipError_t launch_dense(const DenseGemm& g, hipStream_t s) {
 
 hipError_t launch_gate_up(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
     switch (fmt) {
-        case Fmt::Q8_0: return launch_routed<FragQ80, kGateUp>(g, s);
-        case Fmt::Q4_K: return launch_routed<FragQ4K, kGateUp>(g, s);
-        case Fmt::Q2_K: return launch_routed<FragQ2K, kGateUp>(g, s);
+        case Fmt::Q8_0: return launch_routed<FragQ80, kGateUp>(fmt, g, s);
+        case Fmt::Q4_K: return launch_routed<FragQ4K, kGateUp>(fmt, g, s);
+        case Fmt::Q2_K: return launch_routed<FragQ2K, kGateUp>(fmt, g, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
     switch (fmt) {
-        case Fmt::Q8_0: return launch_routed<FragQ80, kDown>(g, s);
-        case Fmt::Q4_K: return launch_routed<FragQ4K, kDown>(g, s);
-        case Fmt::Q2_K: return launch_routed<FragQ2K, kDown>(g, s);
+        case Fmt::Q8_0: return launch_routed<FragQ80, kDown>(fmt, g, s);
+        case Fmt::Q4_K: return launch_routed<FragQ4K, kDown>(fmt, g, s);
+        case Fmt::Q2_K: return launch_routed<FragQ2K, kDown>(fmt, g, s);
         default: return hipErrorInvalidValue;
     }
 }

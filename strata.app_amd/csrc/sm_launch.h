@@ -80,9 +80,18 @@ struct RoutedGemm {
     uint32_t k;                 // reduction length (d for gate/up, I for down)
     uint32_t n_out;             // output columns (I for gate/up, d for down)
     uint64_t row_bytes;         // bytes of one weight row of k values
+    // Groups with at least this many entries run in 256-row units on the wide kernel and are
+    // skipped by the 64-row tile kernels; ~0u: every group runs in 64-row tiles.
+    uint32_t wide_min;
 };
+// Both launch the wide kernel (when g.wide_min != ~0u) and then the 64-row tile kernel.
 hipError_t launch_gate_up(Fmt fmt, const RoutedGemm& g, hipStream_t s);
 hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s);
+// Whether the wide kernel supports a stage: a block format, K a multiple of 64, and whole
+// 256-row column tiles (gate/up: 128 hidden columns, down: 256 output columns).
+bool wide_fits(Fmt fmt, bool gate_up, uint32_t k, uint32_t n_out);
+hipError_t launch_wide(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s);
+constexpr uint32_t kWideMin = 128;
 
 struct DenseGemm {
     const _Float16* a;          // [rows][k]

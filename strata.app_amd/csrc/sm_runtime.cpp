@@ -358,6 +358,7 @@ sm::RoutedGemm gate_up_gemm(const sm_moe_shape& s, int fmt, const GateUpRes& r) 
     g.k = s.hidden;
     g.n_out = s.expert_ff;
     g.row_bytes = fmt_row_bytes(fmt, s.hidden);
+    g.wide_min = sm::wide_fits(Fmt(fmt), true, g.k, g.n_out) ? sm::kWideMin : ~0u;
     return g;
 }
 
@@ -424,6 +425,7 @@ sm::RoutedGemm down_gemm(const sm_moe_shape& s, int fmt, const DownRes& r) {
     g.k = s.expert_ff;
     g.n_out = s.hidden;
     g.row_bytes = fmt_row_bytes(fmt, s.expert_ff);
+    g.wide_min = sm::wide_fits(Fmt(fmt), false, g.k, g.n_out) ? sm::kWideMin : ~0u;
     return g;
 }
 
