@@ -751,6 +751,7 @@ hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
 }
 
 hipError_t launch_dense_gate_up(Fmt fmt, const DenseGemm& g, hipStream_t s) {
+    if (wide_dense_fits(fmt, true, g.rows, g.k, g.n_out)) return launch_wide_dense(fmt, true, g, s);
     switch (fmt) {
         case Fmt::F16: return launch_dense<FragF16, kGateUp>(g, s);
         case Fmt::BF16: return launch_dense<FragBF16, kGateUp>(g, s);
@@ -759,6 +760,7 @@ hipError_t launch_dense_gate_up(Fmt fmt, const DenseGemm& g, hipStream_t s) {
 }
 
 hipError_t launch_dense_down(Fmt fmt, const DenseGemm& g, hipStream_t s) {
+    if (wide_dense_fits(fmt, false, g.rows, g.k, g.n_out)) return launch_wide_dense(fmt, false, g, s);
     switch (fmt) {
         case Fmt::F16: return launch_dense<FragF16, kDown>(g, s);
         case Fmt::BF16: return launch_dense<FragBF16, kDown>(g, s);

@@ -104,6 +104,10 @@ struct DenseGemm {
 };
 hipError_t launch_dense_gate_up(Fmt fmt, const DenseGemm& g, hipStream_t s);
 hipError_t launch_dense_down(Fmt fmt, const DenseGemm& g, hipStream_t s);
+// The dense products on the wide kernel (256-row units of the activation rows): F16/BF16
+// weights, K a multiple of 128, whole column tiles, and enough units for half of the CUs.
+bool wide_dense_fits(Fmt fmt, bool gate_up, uint32_t rows, uint32_t k, uint32_t n_out);
+hipError_t launch_wide_dense(Fmt fmt, bool gate_up, const DenseGemm& g, hipStream_t s);
 // gl[t] = sum_k x[t,k] * gv[k] (F16 or BF16 gate vector), F32 accumulation.
 hipError_t launch_gate_logit(Fmt fmt, const _Float16* x, const uint8_t* gv, float* gl, uint32_t rows,
                              uint32_t d, hipStream_t s);

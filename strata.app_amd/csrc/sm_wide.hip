@@ -175,6 +175,41 @@ struct ProdQ2K {
     }
 };
 
+// F16 rows (dense weights): the chunks are copied as they are.
+struct ProdF16 {
+    static constexpr int kSlab = 512;
+    half8 v[4];
+    __device__ __forceinline__ void load(const uint8_t* sb, uint32_t g, uint32_t b) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            v[s] = ld_global<half8>(sb + 128u * g + 16u * (4u * uint32_t(s >> 1) + 2u * b + uint32_t(s & 1)));
+    }
+    __device__ __forceinline__ void prepare() {}
+    __device__ __forceinline__ half8 chunk(int s) const { return v[s]; }
+};
+
+// BF16 rows (dense weights): widened exactly to F32 and rounded once to F16, as FragBF16.
+struct ProdBF16 {
+    static constexpr int kSlab = 512;
+    u32x4 v[4];
+    __device__ __forceinline__ void load(const uint8_t* sb, uint32_t g, uint32_t b) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            v[s] = ld_global<u32x4>(sb + 128u * g + 16u * (4u * uint32_t(s >> 1) + 2u * b + uint32_t(s & 1)));
+    }
+    __device__ __forceinline__ void prepare() {}
+    __device__ __forceinline__ half8 chunk(int s) const {
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = v[s][i];
+            h[2 * i] = _Float16(__builtin_bit_cast(float, w << 16));
+            h[2 * i + 1] = _Float16(__builtin_bit_cast(float, w & 0xffff0000u));
+        }
+        return h;
+    }
+};
+
 // Chunk (0..7) of the 64-value step that producer part s of thread b writes.
 template <class Prod> struct ChunkIndex {
     static __device__ __forceinline__ uint32_t of(int s, uint32_t b) {
@@ -204,8 +239,11 @@ __device__ void zero_item(const RoutedGemm& g, const Unit& u, uint32_t ct, const
     }
 }
 
-template <class Prod, int MODE>
-__global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, uint32_t n_ct) {
+// DENSE: the rows are the n_entries activation rows themselves (the shared expert), in units
+// of 256 consecutive rows; the weights are dw0/dw1 and the down output row is the unit row.
+template <class Prod, int MODE, bool DENSE>
+__global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, const uint8_t* dw0, const uint8_t* dw1,
+                                                                 uint32_t n_ct) {
     __shared__ __attribute__((aligned(1024))) uint8_t s_a[2][kStageBytes];
     __shared__ __attribute__((aligned(1024))) uint8_t s_b[2][kStageBytes];
     __shared__ uint32_t s_pref[513];  // exclusive prefix of units over groups
@@ -217,6 +255,10 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, u
     const Plan* p = g.plan;
 
     // ---- unit enumeration: groups with >= wide_min entries, ceil(size / 256) units each ----
+    uint32_t U;
+    if (DENSE) {
+        U = (g.n_entries + kUnitRows - 1u) / kUnitRows;
+    } else {
     if (tid == 0) s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t ng = p->n_groups < 512u ? p->n_groups : 512u;
     uint32_t units = 0;
@@ -241,7 +283,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, u
     __syncthreads();
     // An invalid plan or permutation: the 64-row tile kernel zeroes every slot.
     if (s_flag & 2u) return;
-    const uint32_t U = s_pref[512];
+    U = s_pref[512];
+    }
 
     // ---- per-thread constant roles ----
     const uint32_t wave_u = uint32_t(__builtin_amdgcn_readfirstlane(int(wave)));
@@ -265,14 +308,18 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, u
     const uint32_t nK = g.k / kStepK;
     for (uint32_t m = l; m < n_items; m += P) {
         const uint32_t v = m / n_ct, ct = m - v * n_ct, uidx = x + 8u * v;
-        uint32_t lo_g = 0, hi_g = 512;
-        while (hi_g - lo_g > 1u) {
-            const uint32_t mid = (lo_g + hi_g) >> 1;
-            if (s_pref[mid] <= uidx) lo_g = mid;
-            else hi_g = mid;
-        }
         Unit u;
-        {
+        if (DENSE) {
+            u.a0 = kUnitRows * uidx;
+            u.a1 = u.a0 + kUnitRows < g.n_entries ? u.a0 + kUnitRows : g.n_entries;
+            u.ex = 0;
+        } else {
+            uint32_t lo_g = 0, hi_g = 512;
+            while (hi_g - lo_g > 1u) {
+                const uint32_t mid = (lo_g + hi_g) >> 1;
+                if (s_pref[mid] <= uidx) lo_g = mid;
+                else hi_g = mid;
+            }
             const uint32_t f = uint32_t(p->grp_start[lo_g]), e = uint32_t(p->grp_start[lo_g + 1]);
             u.a0 = f + kUnitRows * (uidx - s_pref[lo_g]);
             u.a1 = u.a0 + kUnitRows < e ? u.a0 + kUnitRows : e;
@@ -280,11 +327,15 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, u
         }
         const uint32_t nrows = u.a1 - u.a0;
         __syncthreads();  // the previous item's last reads of LDS are done
-        if (MODE == kDown && tid < kUnitRows) s_dst[tid] = tid < nrows ? g.dst[u.a0 + tid] : -1;
-        const uint64_t* addr = g.addresses + 3u * u.ex;
-        const uint8_t* w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
-        const uint8_t* w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
-        if (w0 == nullptr || w1 == nullptr) {
+        if (!DENSE && MODE == kDown && tid < kUnitRows) s_dst[tid] = tid < nrows ? g.dst[u.a0 + tid] : -1;
+        const uint8_t* w0 = dw0;
+        const uint8_t* w1 = dw1;
+        if (!DENSE) {
+            const uint64_t* addr = g.addresses + 3u * u.ex;
+            w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
+            w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
+        }
+        if (!DENSE && (w0 == nullptr || w1 == nullptr)) {
             __syncthreads();
             if (tid == 0) atomicOr(g.status, 1u);
             zero_item<MODE>(g, u, ct, s_dst);
@@ -422,8 +473,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, u
                     g.out_h[uint64_t(a) * g.n_out + 128u * ct + 32u * cq + r32] =
                         half_sat(silu_fast(acc[rb][0][i]) * acc[rb][1][i]);
                 } else {
-                    const uint32_t d = uint32_t(s_dst[r]);
-                    const bool good = d < g.n_entries;
+                    const uint32_t d = DENSE ? a : uint32_t(s_dst[r]);
+                    const bool good = DENSE || d < g.n_entries;
                     if (!good) atomicOr(g.status, 2u);
                     const uint64_t row = good ? d : a;
 #pragma unroll
@@ -435,8 +486,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, u
     }
 }
 
-template <class Prod, int MODE>
-hipError_t launch_wide_t(const RoutedGemm& g, hipStream_t s) {
+uint32_t wide_cus() {
     static int cus = 0;
     if (cus == 0) {
         int dev = 0, v = 0;
@@ -446,15 +496,42 @@ hipError_t launch_wide_t(const RoutedGemm& g, hipStream_t s) {
         else
             cus = 256;
     }
+    return uint32_t(cus);
+}
+
+// Persistent grid: one workgroup per CU (each holds about 133 KB of LDS), at most one per
+// item, in whole groups of 8 (one per XCD).
+uint32_t wide_blocks(uint64_t max_items) {
+    uint64_t blocks = (max_items + 7u) & ~uint64_t(7);
+    const uint64_t cap = uint64_t(wide_cus()) & ~uint64_t(7);
+    if (blocks > cap) blocks = cap;
+    if (blocks < 8) blocks = 8;
+    return uint32_t(blocks);
+}
+
+template <class Prod, int MODE>
+hipError_t launch_wide_t(const RoutedGemm& g, hipStream_t s) {
     const uint32_t n_ct = MODE == kGateUp ? g.n_out / 128u : g.n_out / 256u;
     // Units are at most n_entries / wide_min (each covers >= wide_min / 2 rows of a group of
     // at least wide_min entries, wide_min >= 128), so small layers launch fewer workgroups.
-    const uint64_t max_items = uint64_t(g.n_entries / g.wide_min + 1u) * n_ct;
-    uint64_t blocks = (max_items + 7u) & ~uint64_t(7);
-    const uint64_t cap = uint64_t(cus) & ~uint64_t(7);
-    if (blocks > cap) blocks = cap;
-    if (blocks < 8) blocks = 8;
-    wide_gemm_kernel<Prod, MODE><<<uint32_t(blocks), kWideThreads, 0, s>>>(g, n_ct);
+    const uint32_t blocks = wide_blocks(uint64_t(g.n_entries / g.wide_min + 1u) * n_ct);
+    wide_gemm_kernel<Prod, MODE, false><<<blocks, kWideThreads, 0, s>>>(g, nullptr, nullptr, n_ct);
+    return hipGetLastError();
+}
+
+template <class Prod, int MODE>
+hipError_t launch_dense_t(const DenseGemm& d, hipStream_t s) {
+    RoutedGemm g{};
+    g.a = d.a;
+    g.out_h = d.out_h;
+    g.out_f = d.out_f;
+    g.n_entries = d.rows;
+    g.k = d.k;
+    g.n_out = d.n_out;
+    g.row_bytes = d.row_bytes;
+    const uint32_t n_ct = MODE == kGateUp ? g.n_out / 128u : g.n_out / 256u;
+    const uint32_t blocks = wide_blocks(uint64_t((d.rows + kUnitRows - 1u) / kUnitRows) * n_ct);
+    wide_gemm_kernel<Prod, MODE, true><<<blocks, kWideThreads, 0, s>>>(g, d.w0, MODE == kGateUp ? d.w1 : d.w0, n_ct);
     return hipGetLastError();
 }
 
@@ -463,6 +540,22 @@ hipError_t launch_wide_t(const RoutedGemm& g, hipStream_t s) {
 bool wide_fits(Fmt fmt, bool gate_up, uint32_t k, uint32_t n_out) {
     if (fmt != Fmt::Q8_0 && fmt != Fmt::Q4_K && fmt != Fmt::Q2_K) return false;
     return k % (2u * kStepK) == 0 && n_out % (gate_up ? 128u : 256u) == 0;
+}
+
+bool wide_dense_fits(Fmt fmt, bool gate_up, uint32_t rows, uint32_t k, uint32_t n_out) {
+    if (fmt != Fmt::F16 && fmt != Fmt::BF16) return false;
+    if (k % (2u * kStepK) != 0 || n_out % (gate_up ? 128u : 256u) != 0) return false;
+    // Worth it once the units keep at least half of the CUs busy.
+    const uint64_t items = uint64_t((rows + kUnitRows - 1u) / kUnitRows) * (gate_up ? n_out / 128u : n_out / 256u);
+    return items * 2u >= wide_cus();
+}
+
+hipError_t launch_wide_dense(Fmt fmt, bool gate_up, const DenseGemm& d, hipStream_t s) {
+    switch (fmt) {
+        case Fmt::F16: return gate_up ? launch_dense_t<ProdF16, kGateUp>(d, s) : launch_dense_t<ProdF16, kDown>(d, s);
+        case Fmt::BF16: return gate_up ? launch_dense_t<ProdBF16, kGateUp>(d, s) : launch_dense_t<ProdBF16, kDown>(d, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_wide(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s) {
