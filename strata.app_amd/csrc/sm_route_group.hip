@@ -13,28 +13,32 @@ constexpr float kWeightFloor = 6.103515625e-5f;  // 2^-14
 // Router GEMM: logits[t,e] = sum_k x[t,k] * W[e,k], F16 activations, F32 weights.
 // Each F32 weight is split into an F16 head and an F16 tail scaled by 2^11
 // (w = hi + lo * 2^-11 to ~2^-24 relative); two MFMA accumulators carry the head and tail
-// products and are merged as fma(lo, 2^-11, hi). Tile: 32 tokens x 64 experts per
-// 256-thread workgroup (two workgroups per CU); wave w owns experts 16w..16w+15. The 32 x
-// 256 activation slab is copied by LDS-DMA into a double-buffered, XOR-swizzled LDS ring;
-// each lane's 64 F32 weights of the next slab are in flight in registers while the current
-// slab is split and multiplied.
+// products and are merged as fma(lo, 2^-11, hi). Tile: ROWS tokens (32, 64 or 128) x 64
+// experts per 256-thread workgroup; wave w owns experts 16w..16w+15. Each expert's weights
+// are read and split once per workgroup, so larger token tiles divide that work; the
+// launcher takes the largest tile that still gives every CU a workgroup. The ROWS x 256
+// activation slab is copied by LDS-DMA into a double-buffered, XOR-swizzled LDS ring; each
+// lane's 64 F32 weights of the next slab are in flight in registers while the current slab
+// is split and multiplied.
 // ---------------------------------------------------------------------------------------
-constexpr int kRouterRows = 32;
 constexpr int kRouterCols = 64;
 constexpr int kSlab = 256;
 
 // Position (16-byte chunks) of chunk c of row r in a swizzled rows x 256 slab.
 __device__ __forceinline__ uint32_t slab_pos(uint32_t r, uint32_t c) { return r * 32u + (c ^ (r & 15u)); }
 
+template <int ROWS>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
                                                           float* __restrict__ logits,
                                                           uint32_t rows, uint32_t d, uint32_t E) {
-    __shared__ __attribute__((aligned(1024))) _Float16 sa[2][kRouterRows * kSlab];
+    constexpr int RB = ROWS / 16;    // 16-row MFMA blocks
+    constexpr int NJ = ROWS / 8;     // activation copy instructions per wave and slab
+    __shared__ __attribute__((aligned(1024))) _Float16 sa[2][ROWS * kSlab];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const uint32_t t0 = blockIdx.x * kRouterRows;
+    const uint32_t t0 = blockIdx.x * ROWS;
     const uint32_t e0 = blockIdx.y * kRouterCols;
     const uint32_t e = e0 + 16 * wave + n;
     const bool e_ok = e < E;
@@ -42,22 +46,24 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
     // so the four lane groups of an expert row read one contiguous 128-byte piece per
     // k-step (row 0 stands in for experts past E; those outputs are never stored).
     const float* wrow = w + uint64_t(e_ok ? e : 0) * d + 8 * g;
-    // Activation copy map: wave instruction q = 4*wave + j fills chunk positions
-    // [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk (lane & 31) ^ (R & 15).
-    const _Float16* asrc[4];
+    // Activation copy map: wave instruction q = NJ*wave + j fills chunk positions
+    // [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk (lane & 31) ^ (R & 15). Row
+    // offsets are kept in halves (rows x d < 2^32 is checked by the launcher).
+    uint32_t aofs[NJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t R = 2u * (4u * wave + j) + (uint32_t(lane) >> 5);
+    for (int j = 0; j < NJ; ++j) {
+        const uint32_t R = 2u * (uint32_t(NJ) * wave + j) + (uint32_t(lane) >> 5);
         const uint32_t C = (uint32_t(lane) & 31u) ^ (R & 15u);
         const uint32_t t = t0 + R < rows ? t0 + R : rows - 1u;
-        asrc[j] = x + uint64_t(t) * d + 8u * C;
+        aofs[j] = t * d + 8u * C;
     }
     auto issue_a = [&](uint32_t k0, _Float16* slab) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
             __builtin_amdgcn_global_load_lds(
-                reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(asrc[j] + k0)),
-                reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(slab + (4 * wave + j) * 512)),
+                reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(x + aofs[j] + k0)),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(slab + (NJ * wave + j) * 512)),
                 16, 0, 0);
     };
     float4v cw[16], nw[16];
@@ -65,9 +71,9 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
 #pragma unroll
         for (int i = 0; i < 16; ++i) dst[i] = ld_global<float4v>(wrow + k0 + 32 * (i >> 1) + 4 * (i & 1));
     };
-    float4v acc_hi[2], acc_lo[2];
+    float4v acc_hi[RB], acc_lo[RB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
+    for (int rb = 0; rb < RB; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
     const uint32_t n_slabs = d / kSlab;
     issue_a(0, sa[0]);
     load_w(0, cw);
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
                 bl[i] = _Float16((wf - float(h)) * 2048.0f);
             }
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const half8 a = *reinterpret_cast<const half8*>(buf + 8u * slab_pos(16u * rb + n, 4u * s + g));
                 acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_hi[rb], 0, 0, 0);
                 acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_lo[rb], 0, 0, 0);
@@ -102,7 +108,7 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
     if (!e_ok) return;
     const float b = bias != nullptr ? bias[e] : 0.0f;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t t = t0 + 16 * rb + 4 * g + i;
@@ -479,8 +485,18 @@ __global__ __launch_bounds__(256) void destination_validate_kernel(const int32_t
 
 hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bias, float* logits,
                               uint32_t rows, uint32_t d, uint32_t E, hipStream_t s) {
-    const dim3 grid((rows + kRouterRows - 1) / kRouterRows, (E + kRouterCols - 1) / kRouterCols);
-    router_gemm_kernel<<<grid, 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+    // The largest token tile that still launches at least one workgroup per CU (256), so
+    // each expert's weights are split as few times as the layer allows.
+    const uint32_t ecols = (E + kRouterCols - 1) / kRouterCols;
+    const bool fits = uint64_t(rows) * d < (1ull << 32);
+    auto blocks = [&](uint32_t r) { return ((rows + r - 1) / r) * ecols; };
+    if (fits && blocks(128) >= 256u) {
+        router_gemm_kernel<128><<<dim3((rows + 127) / 128, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+    } else if (fits && blocks(64) >= 256u) {
+        router_gemm_kernel<64><<<dim3((rows + 63) / 64, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+    } else {
+        router_gemm_kernel<32><<<dim3((rows + 31) / 32, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+    }
     return hipGetLastError();
 }
 
