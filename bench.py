@@ -211,7 +211,10 @@ def main() -> int:
     else:
         roof = {"bound": "mfma", "achieved": round(gu_tflops, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(gu_tflops / F16_MFMA_PEAK_TFLOPS, 4)}
-    kernel = f"routed_gemm_staged_kernel<Frag{moe.FORMAT_NAMES[cfg.gate_up_fmt].replace('_', '')}, gate/up>"
+    fmt_tag = moe.FORMAT_NAMES[cfg.gate_up_fmt].replace('_', '')
+    # The stage is two launches: the wide kernel (groups >= 128 entries) and the 64-row tile
+    # kernel; kernel_us, traffic and the algorithmic bytes all cover both.
+    kernel = f"gate/up stage: routed_gemm_staged_kernel<Frag{fmt_tag}> + wide_gemm_kernel<Prod{fmt_tag}>"
     roof.update({"kernel": kernel, "kernel_us": round(gu_kernel_ms * 1e3, 2),
                  "traffic": traffic_bytes(args.config, "gate_up"),
                  "algorithmic_bytes": gu_bytes, "algorithmic_flops": gu_flops,
