@@ -345,34 +345,54 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(const int32_t* __res
     dst[slot] = int32_t(entry);
 }
 
-// Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. A workgroup copies kGatherRows
-// grouped rows; a row's source index is workgroup-uniform, and each thread issues its loads
-// for all rows before its stores (16 bytes each). The stores are non-temporal: the grouped rows
-// are a write-once stream. The plan header is checked first as in the reference's gather
-// (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
-constexpr uint32_t kGatherRows = 4;
+// Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. Workgroup b copies the rows of
+// grouped chunk b / 8 (kGatherChunk rows) whose source token lies in token slice b % 8
+// (tokens [T*s/8, T*(s+1)/8)). Every (chunk, slice) pair belongs to one workgroup, so each
+// row is written exactly once whatever the placement; workgroups are placed round-robin on
+// the 8 XCDs, so each XCD reads only its eighth of X and keeps it in its own L2 (each token
+// row is read top-k times). Wave 0 compacts the chunk's rows of its slice into LDS; the
+// workgroup then copies them kGatherRows at a time, 16 bytes per thread, each thread
+// issuing its loads for those rows before its stores. The stores are non-temporal: the
+// grouped rows are a write-once stream. The plan header is checked first as in the
+// reference's gather (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
+constexpr uint32_t kGatherChunk = 64, kGatherRows = 4;
 __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t rows,
                                                      uint32_t vpr, const int32_t* __restrict__ src,
                                                      const Plan* __restrict__ plan, uint32_t N,
                                                      u32x4* __restrict__ xs) {
+    static_assert(kGatherChunk == 64, "one wave compacts a chunk");
+    __shared__ uint32_t s_row[kGatherChunk], s_tok[kGatherChunk], s_n;
+    const uint32_t tid = threadIdx.x, slice = blockIdx.x & 7u, a = (blockIdx.x >> 3) * kGatherChunk + tid;
+    const uint32_t t_lo = uint32_t((uint64_t(rows) * slice) >> 3);
+    const uint32_t t_hi = uint32_t((uint64_t(rows) * (slice + 1u)) >> 3);
+    const int32_t sv = tid < kGatherChunk && a < N ? src[a] : -1;  // issued before the plan reads
     const uint32_t ng = plan->n_groups;
     if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) return;
     const int32_t sorted_signed = plan->grp_start[ng];
     if (sorted_signed < 0 || uint32_t(sorted_signed) != N - plan->bad) return;
     const uint32_t sorted = uint32_t(sorted_signed);
-    const uint32_t a0 = blockIdx.x * kGatherRows;
-    int32_t s[kGatherRows];
-#pragma unroll
-    for (uint32_t r = 0; r < kGatherRows; ++r) s[r] = a0 + r < sorted ? src[a0 + r] : -1;
-    for (uint32_t c = threadIdx.x; c < vpr; c += 256u) {
-        u32x4 v[kGatherRows];
-#pragma unroll
-        for (uint32_t r = 0; r < kGatherRows; ++r)
-            if (s[r] >= 0 && uint32_t(s[r]) < rows) v[r] = x[uint64_t(uint32_t(s[r])) * vpr + c];
-#pragma unroll
-        for (uint32_t r = 0; r < kGatherRows; ++r)
-            if (s[r] >= 0 && uint32_t(s[r]) < rows) __builtin_nontemporal_store(v[r], &xs[uint64_t(a0 + r) * vpr + c]);
+    if (tid < kGatherChunk) {
+        const bool mine = a < sorted && sv >= 0 && uint32_t(sv) >= t_lo && uint32_t(sv) < t_hi;
+        const uint64_t m = __ballot(mine);
+        if (mine) {
+            const uint32_t pos = uint32_t(__popcll(m & ((1ull << tid) - 1ull)));
+            s_row[pos] = a;
+            s_tok[pos] = uint32_t(sv);
+        }
+        if (tid == 0) s_n = uint32_t(__popcll(m));
     }
+    __syncthreads();
+    const uint32_t n = s_n;
+    for (uint32_t i = 0; i < n; i += kGatherRows)
+        for (uint32_t c = tid; c < vpr; c += 256u) {
+            u32x4 v[kGatherRows];
+#pragma unroll
+            for (uint32_t r = 0; r < kGatherRows; ++r)
+                if (i + r < n) v[r] = x[uint64_t(s_tok[i + r]) * vpr + c];
+#pragma unroll
+            for (uint32_t r = 0; r < kGatherRows; ++r)
+                if (i + r < n) __builtin_nontemporal_store(v[r], &xs[uint64_t(s_row[i + r]) * vpr + c]);
+        }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -526,7 +546,7 @@ hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32
 hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
                          const Plan* plan, uint32_t N, _Float16* xs, hipStream_t s) {
     const uint32_t vpr = d / 8;
-    const uint32_t blocks = (N + kGatherRows - 1) / kGatherRows;
+    const uint32_t blocks = 8u * ((N + kGatherChunk - 1) / kGatherChunk);  // (chunk, token slice) pairs
     gather_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
                                          reinterpret_cast<u32x4*>(xs));
     return hipGetLastError();
