@@ -38,6 +38,13 @@ struct sm_context {
     bool ring_claimed[kRingSlots] = {};  // filled by an encode whose segment is not committed yet
     uint32_t ring_next = 0;
     std::mutex ring_mu;
+    // Second stream (default priority) for launches that depend on nothing recorded before
+    // them in their segment (the shared expert of a full layer): they start behind a fork
+    // event recorded on the caller's stream when the segment is committed, and a later step
+    // marked `join` waits for them. side_mu keeps one commit's event records and waits together.
+    hipStream_t side = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    std::mutex side_mu;
 };
 
 namespace {
@@ -53,6 +60,8 @@ struct sm_segment {
         const char* label;
         std::function<hipError_t(hipStream_t)> run;
         int ring_slot = -1, ring_slot2 = -1;
+        bool side = false;  // runs on the context's side stream (untimed commits)
+        bool join = false;  // waits for every side launch recorded before it
     };
     std::vector<Step> steps;
     bool failed = false;
@@ -196,8 +205,11 @@ sm_status record_fail(sm_segment* seg, sm_status st, const std::string& err) {
     return st;
 }
 
-void add_step(sm_segment* seg, const char* label, std::function<hipError_t(hipStream_t)> fn) {
+void add_step(sm_segment* seg, const char* label, std::function<hipError_t(hipStream_t)> fn, bool side = false,
+              bool join = false) {
     seg->steps.push_back({label, std::move(fn)});
+    seg->steps.back().side = side;
+    seg->steps.back().join = join;
 }
 
 // ---- stage encoders (validation + deferred launches) --------------------------------
@@ -507,7 +519,9 @@ bool check_shared(Check& c, const sm_moe_shape& s, int fmt, const sm_shared_buff
            c.view(b.gate_logit, uint64_t(s.rows) * 4, 4, "gate logit", true, r.gl);
 }
 
-void encode_shared_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r) {
+// side: the launches go to the context's side stream (a full layer, where nothing before
+// them in the segment writes what they read).
+void encode_shared_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r, bool side = false) {
     sm::DenseGemm gu{};
     gu.a = reinterpret_cast<const _Float16*>(r.x);
     gu.w0 = reinterpret_cast<const uint8_t*>(r.wg);
@@ -527,12 +541,12 @@ void encode_shared_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const
     dn.row_bytes = 2ull * s.shared_ff;
     const auto rows = s.rows, d = s.hidden;
     const uintptr_t x = r.x, gv = r.gv, gl = r.gl;
-    add_step(seg, "shared gate/up", [=](hipStream_t st) { return sm::launch_dense_gate_up(Fmt(fmt), gu, st); });
-    add_step(seg, "shared down", [=](hipStream_t st) { return sm::launch_dense_down(Fmt(fmt), dn, st); });
+    add_step(seg, "shared gate/up", [=](hipStream_t st) { return sm::launch_dense_gate_up(Fmt(fmt), gu, st); }, side);
+    add_step(seg, "shared down", [=](hipStream_t st) { return sm::launch_dense_down(Fmt(fmt), dn, st); }, side);
     add_step(seg, "shared gate logit", [=](hipStream_t st) {
         return sm::launch_gate_logit(Fmt(fmt), reinterpret_cast<const _Float16*>(x), reinterpret_cast<const uint8_t*>(gv),
                                      reinterpret_cast<float*>(gl), rows, d, st);
-    });
+    }, side);
 }
 
 struct CombineRes { uintptr_t parts, weights, shared, gate, out; };
@@ -550,13 +564,13 @@ bool check_combine(Check& c, const sm_moe_shape& s, const sm_combine_buffers& b,
     return ok && c.view(b.output, o_b, 16, "output", true, r.out);
 }
 
-void encode_combine_launch(sm_segment* seg, const sm_moe_shape& s, const CombineRes& r) {
+void encode_combine_launch(sm_segment* seg, const sm_moe_shape& s, const CombineRes& r, bool join = false) {
     const auto rows = s.rows, K = s.top_k, d = s.hidden;
     add_step(seg, "combine", [=](hipStream_t st) {
         return sm::launch_combine(reinterpret_cast<const float*>(r.parts), reinterpret_cast<const float*>(r.weights),
                                   reinterpret_cast<const float*>(r.shared), reinterpret_cast<const float*>(r.gate),
                                   reinterpret_cast<float*>(r.out), rows, K, d, st);
-    });
+    }, false, join);
 }
 
 const char* const kRingFull =
@@ -634,6 +648,9 @@ sm_status sm_context_create(int device, sm_context** out) {
                                 hipHostMallocDefault) == hipSuccess;
         for (uint32_t i = 0; ok && i < sm_context::kRingSlots; ++i)
             ok = hipEventCreateWithFlags(&c->ring_ev[i], hipEventDisableTiming) == hipSuccess;
+        ok = ok && hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) == hipSuccess &&
+             hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming) == hipSuccess;
         if (!ok) {
             sm_context_destroy(c);
             return SM_E_DEVICE;
@@ -652,6 +669,12 @@ void sm_context_destroy(sm_context* ctx) {
         (void)hipEventDestroy(ctx->ring_ev[i]);
     }
     if (ctx->ring) (void)hipHostFree(ctx->ring);
+    if (ctx->side) {
+        (void)hipStreamSynchronize(ctx->side);
+        (void)hipStreamDestroy(ctx->side);
+    }
+    if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+    if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
     delete ctx;
 }
 
@@ -682,25 +705,50 @@ sm_status sm_segment_begin(sm_context* ctx, sm_segment** out) {
 namespace {
 
 // Runs the recorded launches in order on `stream`. With `ev` (two events per launch), each
-// launch is bracketed by event records for sm_segment_commit_timed.
+// launch is bracketed by event records for sm_segment_commit_timed, and every launch runs
+// on `stream`. Without it, side steps run on the context's side stream: it waits for a fork
+// event recorded on `stream` before the first launch, and `stream` waits for a join event
+// recorded on the side stream before each join step and, if side launches follow the last
+// join, at the end, so the caller's stream orders after all of the segment's work.
 sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
     sm_status st = SM_OK;
-    if (!seg->ctx->has_device || hipSetDevice(seg->ctx->device) != hipSuccess) st = SM_E_DEVICE;
+    sm_context* ctx = seg->ctx;
+    if (!ctx->has_device || hipSetDevice(ctx->device) != hipSuccess) st = SM_E_DEVICE;
+    bool use_side = false;
+    for (const auto& step : seg->steps) use_side = use_side || (step.side && ev == nullptr);
+    std::unique_lock<std::mutex> side_lk(ctx->side_mu, std::defer_lock);
+    if (use_side) {
+        side_lk.lock();
+        if (st == SM_OK && (hipEventRecord(ctx->fork_ev, stream) != hipSuccess ||
+                            hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0) != hipSuccess))
+            st = SM_E_DEVICE;
+    }
+    bool side_open = false;  // side launches not yet joined
+    auto join = [&]() {
+        if (st == SM_OK && (hipEventRecord(ctx->join_ev, ctx->side) != hipSuccess ||
+                            hipStreamWaitEvent(stream, ctx->join_ev, 0) != hipSuccess))
+            st = SM_E_DEVICE;
+        side_open = false;
+    };
     for (size_t i = 0; i < seg->steps.size(); ++i) {
         auto& step = seg->steps[i];
         if (st != SM_OK) break;
-        if (ev && hipEventRecord(ev[2 * i], stream) != hipSuccess) st = SM_E_DEVICE;
-        if (st == SM_OK && step.run(stream) != hipSuccess) st = SM_E_DEVICE;
-        if (st == SM_OK && ev && hipEventRecord(ev[2 * i + 1], stream) != hipSuccess) st = SM_E_DEVICE;
+        if (step.join && side_open) join();
+        const hipStream_t hs = use_side && step.side ? ctx->side : stream;
+        side_open = side_open || hs != stream;
+        if (st == SM_OK && ev && hipEventRecord(ev[2 * i], hs) != hipSuccess) st = SM_E_DEVICE;
+        if (st == SM_OK && step.run(hs) != hipSuccess) st = SM_E_DEVICE;
+        if (st == SM_OK && ev && hipEventRecord(ev[2 * i + 1], hs) != hipSuccess) st = SM_E_DEVICE;
         for (const int slot : {step.ring_slot, step.ring_slot2}) {
             if (slot < 0) continue;
-            std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
-            if (hipEventRecord(seg->ctx->ring_ev[slot], stream) == hipSuccess)
-                seg->ctx->ring_pending[slot] = true;
+            std::lock_guard<std::mutex> lk(ctx->ring_mu);
+            if (hipEventRecord(ctx->ring_ev[slot], hs) == hipSuccess)
+                ctx->ring_pending[slot] = true;
             else
                 st = SM_E_DEVICE;
         }
     }
+    if (side_open) join();
     release_ring_slots(seg);
     return st;
 }
@@ -987,10 +1035,12 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
             if (expected_edge(w, r)) continue;
             return record_fail(seg, SM_E_ALIAS, std::string(P) + " " + w.name + " overlaps active " + r.name);
         }
+    // The shared expert reads only the activations and its weights, which no earlier launch
+    // writes (checked above), so it runs beside routing and the routed experts; combine joins.
     encode_route_gather_launch(seg, s, rr, ro, gr);
-    if (has_shared) encode_shared_launch(seg, s, f->shared, sr);
+    if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
     if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
-    encode_combine_launch(seg, s, co);
+    encode_combine_launch(seg, s, co, has_shared);
     return SM_OK;
 }
 
