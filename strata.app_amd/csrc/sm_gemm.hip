@@ -15,15 +15,13 @@
 
 #include "sm_device.h"
 #include "sm_launch.h"
+#include "sm_tiles.h"
 
 namespace sm {
 namespace {
 
 constexpr int kRows = 64;
-constexpr int kSlab = 256;
 constexpr int kLdsRow = kSlab + 8;  // halves
-
-enum Mode { kGateUp = 0, kDown = 1 };
 
 // Hardware dispatches workgroup b to XCD b % 8. Give each XCD a contiguous run of the
 // `real` work items (so the column tiles of one row tile share an XCD's L2), spread over
@@ -232,376 +230,6 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
         }
 }
 
-// ---------------------------------------------------------------------------------------
-// Routed products, staged: 512-thread workgroups (8 waves) over a 64-row tile and `npi`
-// consecutive column tiles. Each wave owns NF 16-column weight fragments (NF = 2 or 4) and
-// all 64 rows, so one column tile covers 128*NF weight rows (gate/up: 64*NF gate rows and
-// the 64*NF up rows of the same hidden columns; down: 128*NF output columns). Per (column
-// tile, slab) step the 64 x 256 activation slab and the weight-row slabs are copied
-// global -> LDS by LDS-DMA (global_load_lds), one step ahead and interleaved with the
-// multiplies; lanes then read their raw fragments from LDS, decode them into the MFMA B
-// layout and multiply against A fragments from the XOR-swizzled activation slab. The steps
-// of a workgroup form one flat pipeline, so short reductions (down: K = I) do not drain it
-// between column tiles.
-// ---------------------------------------------------------------------------------------
-constexpr int kV2Threads = 512;
-
-// Position (in 16-byte chunks) of chunk c of row r inside a swizzled 64 x 256 slab: the
-// 16 rows one MFMA A-fragment read touches map to 16 distinct 4-bank groups.
-__device__ __forceinline__ uint32_t a_pos(uint32_t r, uint32_t c) { return r * 32u + (c ^ (r & 15u)); }
-
-template <int MODE>
-__device__ void zero_cols(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_t c0, uint32_t c1, bool by_dst) {
-    const uint32_t width = c1 - c0;
-    for (uint32_t i = threadIdx.x; i < 64u * width; i += blockDim.x) {
-        const uint32_t r = r0 + i / width, c = c0 + i % width;
-        if (r >= r1 || r >= g.n_entries) continue;
-        if (MODE == kGateUp) {
-            g.out_h[uint64_t(r) * g.n_out + c] = _Float16(0.0f);
-        } else if (!by_dst) {
-            g.out_f[uint64_t(r) * g.n_out + c] = 0.0f;
-        } else {
-            const uint32_t d = uint32_t(g.dst[r]);
-            if (d < g.n_entries) g.out_f[uint64_t(d) * g.n_out + c] = 0.0f;
-            else atomicOr(g.status, 2u);
-        }
-    }
-}
-
-// The work item of one staged workgroup: tile rows [a0, a1) of one expert group and column
-// tiles [nt_begin, nt_end), with the expert's two weight matrices.
-struct TileWork {
-    uint32_t a0, a1, nt_begin, nt_end;
-    const uint8_t* w0;
-    const uint8_t* w1;
-};
-
-// Tile enumeration of the persistent staged kernels (512 threads), once per workgroup:
-// reads the status word and counts, per plan group below wide_min entries, its
-// ceil(size / 64) tiles; s_pref[gi] = tiles of the groups before gi. The plan has been
-// checked against the tile list by the plan validator, so these are exactly the list's
-// tiles of those groups, in order. A group that fails the range checks contributes no
-// tiles and reports status bit 1 (it cannot occur behind a passed plan check). Returns the
-// status word read at start.
-__device__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag) {
-    const Plan* p = g.plan;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t ng = p->n_groups < 512u ? p->n_groups : 512u;
-    uint32_t n = 0;
-    if (tid < ng) {
-        const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
-        if (f >= 0 && e > f && uint32_t(e) <= g.n_entries && ex >= 0 && uint32_t(ex) < g.n_experts) {
-            if (uint32_t(e - f) < g.wide_min) n = (uint32_t(e - f) + 63u) / 64u;
-        } else {
-            atomicOr(g.status, 2u);
-        }
-    }
-#pragma unroll
-    for (uint32_t off = 1; off < 64u; off <<= 1) {
-        const uint32_t y = __shfl_up(n, off);
-        if (lane >= off) n += y;
-    }
-    if (lane == 63u) s_wsum[wave] = n;
-    __syncthreads();
-    uint32_t base = 0;
-    for (uint32_t w = 0; w < wave; ++w) base += s_wsum[w];
-    s_pref[tid + 1] = base + n;
-    if (tid == 0) s_pref[0] = 0;
-    __syncthreads();
-    return *s_flag;
-}
-
-// Item `item` (tile k = item / n_chunks of the enumeration, column chunk item % n_chunks):
-// its rows, column tiles and weights. Returns false when the item is done already: an
-// expert without weights has zeroed its rows and set status bit 0. Uniform per workgroup.
-template <int MODE>
-__device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item, uint32_t n_ntiles,
-                            uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t) {
-    const Plan* p = g.plan;
-    const uint32_t k = item / n_chunks, chunk = item - k * n_chunks;
-    uint32_t lo = 0, hi = 512;
-    while (hi - lo > 1u) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (s_pref[mid] <= k) lo = mid;
-        else hi = mid;
-    }
-    const uint32_t f = uint32_t(p->grp_start[lo]), e = uint32_t(p->grp_start[lo + 1]);
-    const uint32_t ex = uint32_t(p->grp_e[lo]);
-    t.nt_begin = chunk * npi;
-    t.nt_end = t.nt_begin + npi < n_ntiles ? t.nt_begin + npi : n_ntiles;
-    t.a0 = f + 64u * (k - s_pref[lo]);
-    t.a1 = t.a0 + 64u < e ? t.a0 + 64u : e;
-    const uint64_t* addr = g.addresses + 3u * ex;
-    t.w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
-    t.w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
-    if (t.w0 == nullptr || t.w1 == nullptr) {
-        if (threadIdx.x == 0) atomicOr(g.status, 1u);
-        zero_cols<MODE>(g, t.a0, t.a1, t.nt_begin * out_per_nt, t.nt_end * out_per_nt, MODE == kDown);
-        return false;
-    }
-    return true;
-}
-
-// Activation copy map of one 64 x 256 slab: wave instruction q = 4*wave + j (j = 0..3)
-// fills chunk positions [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk
-// C = (lane & 31) ^ (R & 15). Rows past the tile's end repeat its last row.
-__device__ __forceinline__ void slab_sources(const RoutedGemm& g, const TileWork& t, int wave, int lane,
-                                             const _Float16* (&asrc)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t R = 2u * (4u * wave + j) + (uint32_t(lane) >> 5);
-        const uint32_t C = (uint32_t(lane) & 31u) ^ (R & 15u);
-        uint32_t row = t.a0 + R;
-        if (row > t.a1 - 1u) row = t.a1 - 1u;
-        asrc[j] = g.a + uint64_t(row) * g.k + 8u * C;
-    }
-}
-
-// Issues LDS-DMA copy j (0..3, 16 B per lane) of this wave's share of the slab at k0.
-__device__ __forceinline__ void issue_slab_part(const _Float16* const (&asrc)[4], uint32_t k0, _Float16* slab,
-                                                int wave, int j) {
-    __builtin_amdgcn_global_load_lds(
-        reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(asrc[j] + k0)),
-        reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(slab + (4 * wave + j) * 512)),
-        16, 0, 0);
-}
-__device__ __forceinline__ void issue_slab(const _Float16* const (&asrc)[4], uint32_t k0, _Float16* slab, int wave) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) issue_slab_part(asrc, k0, slab, wave, j);
-}
-
-// Geometry of a staged step with NF fragments per wave.
-template <int MODE, int NF>
-struct Staged {
-    static constexpr uint32_t kImageRows = 128u * NF;                          // weight rows per step
-    static constexpr uint32_t kHalf = 64u * NF;                                // gate/up: gate rows, then up rows
-    static constexpr uint32_t kOut = MODE == kGateUp ? 64u * NF : 128u * NF;   // output columns per column tile
-    // Column of lane n's fragment f within the column tile (gate/up: the hidden column, the
-    // same for gate fragment f and up fragment f + NF/2). Down interleaves the fragments, so
-    // lane n holds NF adjacent output columns and 16 lanes store whole 128-byte row pieces.
-    __device__ static __forceinline__ uint32_t col(int wave, int n, int f) {
-        if (MODE == kGateUp) return uint32_t(wave) * (8u * NF) + 16u * uint32_t(f % (NF / 2)) + uint32_t(n);
-        return uint32_t(wave) * (16u * NF) + NF * uint32_t(n) + uint32_t(f);
-    }
-    // Row of the packed weight image holding that fragment.
-    __device__ static __forceinline__ uint32_t image_row(int wave, int n, int f) {
-        if (MODE == kGateUp) return (f < NF / 2 ? 0u : kHalf) + col(wave, n, f);
-        return col(wave, n, f);
-    }
-};
-
-// One 256-value slab of the wave's block. Only the first RB 16-row blocks of the tile hold
-// entries (the rest of a 64-row tile past its group's end would multiply padding), so the
-// others are skipped. after_s(s) runs after k-step s: the staged kernel issues part s of
-// the next step's copies there, so a wave never blocks on a long burst of memory
-// instructions while it could be multiplying.
-template <class Frag, int NF, int RB, class After>
-__device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag (&c)[NF],
-                                         float4v (&acc)[NF][4], After after_s) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        half8 b[NF];
-#pragma unroll
-        for (int f = 0; f < NF; ++f) b[f] = c[f].step(s);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const half8 a = *reinterpret_cast<const half8*>(buf + 8u * a_pos(16u * rb + n, 8u * gq + s));
-#pragma unroll
-            for (int f = 0; f < NF; ++f) acc[f][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[f], acc[f][rb], 0, 0, 0);
-        }
-        after_s(s);
-    }
-}
-
-// Writes a finished column tile and clears the accumulators. gate/up: eh[a][col] =
-// half_sat(silu(gate) * up); down: parts[dst[a]][col], with a destination outside [0, N)
-// reported (status bit 1) and the entry's own row zeroed instead.
-template <int MODE, int NF, int RB>
-__device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint32_t* s_dst, uint32_t a0, uint32_t a1,
-                                                uint32_t col0, int wave, int n, int gq, float4v (&acc)[NF][4]) {
-    using S = Staged<MODE, NF>;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t a = a0 + 16u * rb + 4u * gq + i;
-            if (a >= a1) continue;
-            if (MODE == kGateUp) {
-#pragma unroll
-                for (int f = 0; f < NF / 2; ++f)
-                    g.out_h[uint64_t(a) * g.n_out + col0 + S::col(wave, n, f)] =
-                        half_sat(silu_fast(acc[f][rb][i]) * acc[f + NF / 2][rb][i]);
-            } else {
-                const uint32_t d = s_dst[16 * rb + 4 * gq + i];
-                const bool good = d < g.n_entries;
-                if (!good) atomicOr(g.status, 2u);
-                const uint64_t row = good ? d : a;
-                typedef float vecf __attribute__((ext_vector_type(NF)));
-                vecf v;
-#pragma unroll
-                for (int f = 0; f < NF; ++f) v[f] = good ? acc[f][rb][i] : 0.0f;
-                *reinterpret_cast<vecf*>(g.out_f + row * g.n_out + col0 + S::col(wave, n, 0)) = v;
-            }
-        }
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
-}
-
-// Bytes moved per lane by one LDS-DMA copy of weight-row slabs: 16 where the slab size
-// allows, else 4 (Q2_K's 84-byte slabs). Lane l of a copy writes at LDS base + l * size.
-template <int SB> struct ChunkBytes { static constexpr int value = SB % 16 == 0 ? 16 : 4; };
-
-// The weight-row slabs of one (column tile, slab) step are copied into an LDS image packed
-// as [128*NF rows][SB bytes] by LDS-DMA: wave instruction q moves the 64 consecutive chunks
-// [64q, 64q + 64) of that image, so each instruction reads a few whole row slabs
-// (contiguous bytes) instead of 64 scattered fragments. gate/up: image rows [0, 64*NF) are
-// gate rows nt*64*NF + r, the rest the up rows of the same hidden columns; down: rows
-// nt*128*NF + r. Every instruction is full (128*NF rows x SB/CS chunks is a multiple of 64)
-// and lies wholly in the gate or the up half. Wave w issues instructions q = w + 8j;
-// `off` keeps each lane's byte offset within its matrix for column tile 0, slab 0.
-template <class Frag, int MODE, int NF>
-struct WeightCopy {
-    static constexpr int SB = SlabBytes<Frag>::value;
-    static constexpr int CS = ChunkBytes<SB>::value;
-    static constexpr uint32_t kPerRow = SB / CS;
-    static constexpr uint32_t kInstr = Staged<MODE, NF>::kImageRows * kPerRow / 64u;
-    static constexpr uint32_t kPerWave = (kInstr + 7u) / 8u;
-    static_assert((Staged<MODE, NF>::kImageRows * kPerRow) % 128u == 0u, "copies must be whole wave instructions");
-    uint32_t off[kPerWave];
-    __device__ __forceinline__ void init(const RoutedGemm& g, int wave, int lane) {
-#pragma unroll
-        for (uint32_t j = 0; j < kPerWave; ++j) {
-            const uint32_t c = 64u * (uint32_t(wave) + 8u * j) + uint32_t(lane);
-            uint32_t r = c / kPerRow;
-            const uint32_t piece = c - r * kPerRow;
-            if (MODE == kGateUp && r >= Staged<MODE, NF>::kHalf) r -= Staged<MODE, NF>::kHalf;
-            off[j] = r * g.row_bytes + piece * CS;  // < 512 rows x row_bytes: 32 bits suffice
-        }
-    }
-    // Issues item j (instruction q = wave + 8j) of the copy for (nt, sb) into `wbuf`.
-    __device__ __forceinline__ void issue(const RoutedGemm& g, const TileWork& t, uint32_t nt, uint32_t sb,
-                                          uint8_t* wbuf, int wave, uint32_t j) const {
-        const uint32_t q = uint32_t(wave) + 8u * j;
-        if (q >= kInstr) return;
-        const bool up = MODE == kGateUp && q >= kInstr / 2u;
-        const uint8_t* base = up ? t.w1 : t.w0;
-        const uint32_t rows_per_tile = MODE == kGateUp ? Staged<MODE, NF>::kHalf : Staged<MODE, NF>::kImageRows;
-        const uint64_t tile_off = uint64_t(nt) * rows_per_tile * g.row_bytes + uint64_t(sb) * SB;
-        const uint8_t* src = base + tile_off + off[j];
-        auto* gsrc = reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(src));
-        auto* ldst = reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(wbuf + q * 64u * CS));
-        if constexpr (CS == 16) __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
-        else __builtin_amdgcn_global_load_lds(gsrc, ldst, 4, 0, 0);
-    }
-};
-
-// Weight images per workgroup: two (one filled while the other is read) when they fit
-// beside the activation double buffer within 140 KB of LDS, else one, read into registers
-// behind a second barrier before it is refilled.
-template <class Frag, int NF>
-struct StagedBuffers {
-    static constexpr uint32_t kImage = 128u * NF * SlabBytes<Frag>::value;
-    static constexpr int kWBuf = 65536u + 2u * kImage <= 143360u ? 2 : 1;
-    static_assert(65536u + kImage <= 143360u, "weight image too large for LDS");
-};
-
-// RESIDENT (K <= 512): both activation slabs are copied once and stay in LDS for all of
-// the workgroup's column tiles, instead of being re-read from L2 for each of them.
-template <class Frag, int MODE, int NF, bool RESIDENT>
-__global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGemm g, uint32_t n_ntiles, uint32_t npi,
-                                                                        uint32_t n_chunks) {
-    using S = Staged<MODE, NF>;
-    using WC = WeightCopy<Frag, MODE, NF>;
-    constexpr int SB = SlabBytes<Frag>::value;
-    constexpr int WBUF = StagedBuffers<Frag, NF>::kWBuf;
-    __shared__ __attribute__((aligned(1024))) _Float16 sa[2][64 * kSlab];
-    __shared__ __attribute__((aligned(1024))) uint8_t sw[WBUF][StagedBuffers<Frag, NF>::kImage];
-    __shared__ uint32_t s_dst[64];  // down: destination row of each tile row
-    __shared__ uint32_t s_pref[513], s_wsum[8], s_flag;
-    const uint32_t flag = scan_small_tiles(g, s_pref, s_wsum, &s_flag);
-    if (flag & 2u) {  // invalid plan or permutation: every tile slot writes zeros
-        for (uint32_t slot = blockIdx.x; slot < g.tile_capacity * n_chunks; slot += gridDim.x) {
-            const uint32_t ti = slot / n_chunks, ch = slot % n_chunks;
-            const uint32_t nb = ch * npi, ne = nb + npi < n_ntiles ? nb + npi : n_ntiles;
-            zero_cols<MODE>(g, ti * 64u, ti * 64u + 64u, nb * S::kOut, ne * S::kOut, false);
-        }
-        return;
-    }
-    // Persistent: XCD x (workgroups b with b % 8 == x) takes the contiguous item range
-    // [x * per, (x + 1) * per), so the column chunks of a tile share that XCD's L2.
-    const uint32_t items = s_pref[512] * n_chunks;
-    const uint32_t per = (items + 7u) >> 3, x = blockIdx.x & 7u, P = gridDim.x >> 3;
-    const uint32_t i_end = (x + 1u) * per < items ? (x + 1u) * per : items;
-    for (uint32_t item = x * per + (blockIdx.x >> 3); item < i_end; item += P) {
-    __syncthreads();  // the previous item's reads of LDS are done
-    TileWork t;
-    if (!staged_item<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, S::kOut, t)) continue;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, gq = lane >> 4;
-    // Read once here rather than in each epilogue, where a dependent global load would also
-    // wait for the copies of the next step (visible after the first loop barrier).
-    if (MODE == kDown && tid < 64) s_dst[tid] = t.a0 + uint32_t(tid) < t.a1 ? uint32_t(g.dst[t.a0 + tid]) : ~0u;
-    const uint32_t n_slabs = g.k / kSlab;
-    const uint32_t n_steps = (t.nt_end - t.nt_begin) * n_slabs;
-    const _Float16* asrc[4];
-    slab_sources(g, t, wave, lane, asrc);
-    WC wc;
-    wc.init(g, wave, lane);
-    // Part p (0..7) of the copies of `step`: activation copy p (p < 4, streamed slabs only)
-    // and weight items j with j % 8 == p.
-    auto issue_part = [&](uint32_t step, int p) {
-        const uint32_t nt = t.nt_begin + step / n_slabs, sb = step % n_slabs;
-        if (!RESIDENT && p < 4) issue_slab_part(asrc, sb * kSlab, sa[step & 1u], wave, p);
-        uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
-#pragma unroll
-        for (uint32_t j = uint32_t(p); j < WC::kPerWave; j += 8u) wc.issue(g, t, nt, sb, wb, wave, j);
-    };
-    if (RESIDENT)
-        for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
-#pragma unroll
-    for (int p = 0; p < 8; ++p) issue_part(0, p);
-    // The step loop, specialised on the number of 16-row blocks holding entries.
-    auto run = [&](auto rb_const) {
-        constexpr int RB = decltype(rb_const)::value;
-        float4v acc[NF][4];
-#pragma unroll
-        for (int f = 0; f < NF; ++f)
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
-        for (uint32_t step = 0; step < n_steps; ++step) {
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
-            __syncthreads();                                       // ... from every wave
-            const bool more = step + 1 < n_steps;
-            const uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
-            Frag c[NF];
-#pragma unroll
-            for (int f = 0; f < NF; ++f) c[f].template load<FromLds>(wb + S::image_row(wave, n, f) * SB, gq);
-            // A barrier waits for every outstanding load of the wave, so with one weight image
-            // the next step's copies start only after the second barrier.
-            if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
-#pragma unroll
-            for (int f = 0; f < NF; ++f) c[f].prepare();
-            const uint32_t sb = step % n_slabs;
-            slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [&](int p) {
-                if (more) issue_part(step + 1, p);
-            });
-            if (sb == n_slabs - 1u) {  // column tile complete
-                const uint32_t nt = t.nt_begin + step / n_slabs;
-                staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
-            }
-        }
-    };
-    switch ((t.a1 - t.a0 + 15u) / 16u) {  // workgroup-uniform
-        case 1: run(std::integral_constant<int, 1>()); break;
-        case 2: run(std::integral_constant<int, 2>()); break;
-        case 3: run(std::integral_constant<int, 3>()); break;
-        default: run(std::integral_constant<int, 4>()); break;
-    }
-    }
-}
-
 // Dense (shared-expert) products: rows are tokens in 64-row tiles.
 template <class Frag, int MODE>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseGemm g, uint32_t n_ntiles, uint32_t total) {
@@ -683,33 +311,22 @@ uint32_t device_cus() {
 
 template <class Frag, int MODE, int NF>
 hipError_t launch_staged(const RoutedGemm& g, hipStream_t s) {
-    const uint32_t n_ntiles = g.n_out / Staged<MODE, NF>::kOut;
-    // About 8 (column tile, slab) steps per workgroup; with the activation tile resident
-    // (K <= 512) every column tile of a row tile goes to one workgroup, so the tile is read
-    // once rather than once per workgroup.
-    const uint32_t n_slabs = g.k / kSlab;
-    uint32_t npi = n_slabs <= 2 ? n_ntiles : (n_slabs >= 8 ? 1u : 8u / n_slabs);
-    if (npi > n_ntiles) npi = n_ntiles;
-    const uint32_t n_chunks = (n_ntiles + npi - 1) / npi;
+    const TilePlan p = tile_plan<MODE, NF>(g.k, g.n_out);
     // Persistent: one workgroup per CU (each holds about 130 KB of LDS), never more than the
     // tile slots, in whole groups of 8 (one per XCD).
-    uint32_t blocks = (g.tile_capacity * n_chunks + 7u) & ~7u;
+    uint32_t blocks = (g.tile_capacity * p.n_chunks + 7u) & ~7u;
     const uint32_t cap = device_cus() & ~7u;
     if (blocks > cap) blocks = cap;
     if (blocks < 8u) blocks = 8u;
-    if (n_slabs <= 2)
-        routed_gemm_staged_kernel<Frag, MODE, NF, true><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
+    if (p.resident)
+        routed_gemm_staged_kernel<Frag, MODE, NF, true><<<blocks, kV2Threads, 0, s>>>(g, p.n_ntiles, p.npi, p.n_chunks);
     else
-        routed_gemm_staged_kernel<Frag, MODE, NF, false><<<blocks, kV2Threads, 0, s>>>(g, n_ntiles, npi, n_chunks);
+        routed_gemm_staged_kernel<Frag, MODE, NF, false><<<blocks, kV2Threads, 0, s>>>(g, p.n_ntiles, p.npi, p.n_chunks);
     return hipGetLastError();
 }
 
 template <class Frag, int MODE>
-hipError_t launch_routed(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
-    if (g.wide_min != ~0u) {
-        const hipError_t e = launch_wide(fmt, MODE == kGateUp, g, s);
-        if (e != hipSuccess) return e;
-    }
+hipError_t launch_tiles(const RoutedGemm& g, hipStream_t s) {
     // Two fragments per wave: four (twice the multiplies per activation slab) measured no
     // faster on gfx950 and needs more than 256 VGPRs for Q4_K/Q2_K.
     if (g.k % kSlab == 0 && g.n_out % Staged<MODE, 2>::kOut == 0) return launch_staged<Frag, MODE, 2>(g, s);
@@ -719,6 +336,21 @@ hipError_t launch_routed(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
     if (g.k % kSlab == 0) routed_gemm_kernel<Frag, MODE, true><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
     else routed_gemm_kernel<Frag, MODE, false><<<blocks, 256, 0, s>>>(g, n_ntiles, total);
     return hipGetLastError();
+}
+
+// A stage with wide units. gate/up: one launch of the routed stage kernel (wide units, then
+// the small groups' tiles) where the tiles fit the staged kernel. Down: the wide kernel, then
+// the tile kernel. A down tile item streams a whole expert matrix (8 column tiles) through
+// L2, which evicts the activations that concurrent wide units share across column tiles:
+// with a skewed routing (T = 8192, Zipf 1.1) the single launch measured 460 us against
+// 419 us for the two.
+template <class Frag, int MODE>
+hipError_t launch_routed(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
+    if (g.wide_min == ~0u) return launch_tiles<Frag, MODE>(g, s);
+    if (MODE == kGateUp && g.k % kSlab == 0 && g.n_out % Staged<MODE, 2>::kOut == 0)
+        return launch_stage(fmt, true, g, s);
+    const hipError_t e = launch_wide(fmt, MODE == kGateUp, g, s);
+    return e != hipSuccess ? e : launch_tiles<Frag, MODE>(g, s);
 }
 
 template <class Frag, int MODE>

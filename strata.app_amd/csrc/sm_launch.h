@@ -20,6 +20,13 @@ static_assert(sizeof(Plan) == 6180, "PfPlan layout");
 constexpr uint32_t kCountTile = 256;   // histogram tile (entries)
 constexpr uint32_t kExpertTile = 64;   // tile-list tile (entries)
 constexpr uint32_t kPlanSlotBytes = 6400;
+// The 64-row tile kernels take their work items from per-XCD counters kept in the plan slot's
+// padding after the PfPlan fields: 8 words for gate/up, then 8 for down. Each stage's plan
+// check zeroes them before the stage runs.
+constexpr uint32_t kCounterBytes = 6208;
+constexpr uint32_t kCounterWords = 8;
+static_assert(sizeof(Plan) <= kCounterBytes && kCounterBytes + 2 * 4 * kCounterWords <= kPlanSlotBytes,
+              "counters in the plan slot's padding");
 
 enum class Fmt : int { Q8_0 = 1, Q4_K = 2, Q2_K = 3, F16 = 4, BF16 = 5 };
 
@@ -59,6 +66,8 @@ struct PlanCheck {
     uint32_t snap_words2;
     uint32_t* clear;
     uint32_t clear_words;
+    uint32_t* counters;         // tile-kernel work counters to zero (may be null)
+    uint32_t n_counters;
 };
 hipError_t launch_plan_validate(const PlanCheck& c, hipStream_t s);
 // Checks that `dst` is a permutation of [0, n_entries) with a bitset (zeroed first unless
@@ -67,6 +76,8 @@ hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bitset, uin
                                        uint32_t n_entries, bool bitset_clear, hipStream_t s);
 
 // ---- grouped expert products ----
+enum Mode { kGateUp = 0, kDown = 1 };
+
 struct RoutedGemm {
     const uint64_t* addresses;  // device [E][3] (gate, up, down)
     const _Float16* a;          // grouped rows [N][K]
@@ -83,14 +94,21 @@ struct RoutedGemm {
     // Groups with at least this many entries run in 256-row units on the wide kernel and are
     // skipped by the 64-row tile kernels; ~0u: every group runs in 64-row tiles.
     uint32_t wide_min;
+    uint32_t* counters;         // kCounterWords per-XCD item counters, zeroed by the plan check
 };
-// Both launch the wide kernel (when g.wide_min != ~0u) and then the 64-row tile kernel.
+// Groups of at least g.wide_min entries run on the wide kernel, the others on the 64-row
+// tile kernels; gate/up runs both in one launch where they fit (the routed stage kernel):
+// each workgroup takes its wide units first and then draws tiles, so tiles fill the wide
+// units' tail.
 hipError_t launch_gate_up(Fmt fmt, const RoutedGemm& g, hipStream_t s);
 hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s);
 // Whether the wide kernel supports a stage: a block format, K a multiple of 64, and whole
 // 256-row column tiles (gate/up: 128 hidden columns, down: 256 output columns).
 bool wide_fits(Fmt fmt, bool gate_up, uint32_t k, uint32_t n_out);
 hipError_t launch_wide(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s);
+// One launch for a whole routed gate/up stage: wide units (groups >= g.wide_min), then the
+// other groups' 64-row tiles in the staged form (K a multiple of 256, whole column tiles).
+hipError_t launch_stage(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s);
 constexpr uint32_t kWideMin = 128;
 
 struct DenseGemm {

@@ -406,6 +406,7 @@ __global__ __launch_bounds__(512) void plan_validate_kernel(PlanCheck c) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     for (uint32_t i = blockIdx.x * 512u + tid; i < c.clear_words; i += gridDim.x * 512u) c.clear[i] = 0u;
     if (blockIdx.x != 0) return;
+    if (tid < c.n_counters) c.counters[tid] = 0u;
     // Address snapshots: every load of a thread is issued before its stores, so the reads
     // of pinned host memory cost one round trip (tables are at most 3 x 512 words).
     constexpr int kPer = 3;

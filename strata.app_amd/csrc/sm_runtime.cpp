@@ -371,6 +371,7 @@ sm::RoutedGemm gate_up_gemm(const sm_moe_shape& s, int fmt, const GateUpRes& r) 
     g.n_out = s.expert_ff;
     g.row_bytes = fmt_row_bytes(fmt, s.hidden);
     g.wide_min = sm::wide_fits(Fmt(fmt), true, g.k, g.n_out) ? sm::kWideMin : ~0u;
+    g.counters = reinterpret_cast<uint32_t*>(r.plan + sm::kCounterBytes);
     return g;
 }
 
@@ -386,6 +387,8 @@ sm::PlanCheck stage_check(sm_context* ctx, const sm::RoutedGemm& g, int slot, ui
     c.snap_src = slot >= 0 ? ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
     c.snap_dst = reinterpret_cast<uint64_t*>(snapshot);
     c.snap_words = words;
+    c.counters = g.counters;
+    c.n_counters = sm::kCounterWords;
     return c;
 }
 
@@ -438,6 +441,7 @@ sm::RoutedGemm down_gemm(const sm_moe_shape& s, int fmt, const DownRes& r) {
     g.n_out = s.hidden;
     g.row_bytes = fmt_row_bytes(fmt, s.expert_ff);
     g.wide_min = sm::wide_fits(Fmt(fmt), false, g.k, g.n_out) ? sm::kWideMin : ~0u;
+    g.counters = reinterpret_cast<uint32_t*>(r.plan + sm::kCounterBytes + 4 * sm::kCounterWords);
     return g;
 }
 
@@ -491,6 +495,7 @@ sm_status encode_experts_launch(sm_segment* seg, const sm_moe_shape& s, int fmt_
     c.snap_words2 = c2.snap_words;
     c.clear = reinterpret_cast<uint32_t*>(d.out_f);
     c.clear_words = uint32_t(ceil_div(d.n_entries, 32));
+    c.n_counters = 2 * sm::kCounterWords;  // gate/up's counters, then down's
     add_step(seg, "expert plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
     seg->steps.back().ring_slot = slot1;
     seg->steps.back().ring_slot2 = slot2;

@@ -22,8 +22,11 @@
 // Items are spread XCD-aware: unit u runs on XCD u % 8 (workgroup b runs on XCD b % 8) and
 // the column tiles of a unit are neighbours in that XCD's item order, so they run together
 // and share the unit's activation rows in that XCD's L2.
+#include <type_traits>
+
 #include "sm_device.h"
 #include "sm_launch.h"
+#include "sm_tiles.h"
 
 namespace sm {
 namespace {
@@ -32,8 +35,6 @@ constexpr int kWideThreads = 512;
 constexpr uint32_t kUnitRows = 256;
 constexpr uint32_t kStepK = 64;
 constexpr uint32_t kStageBytes = 256u * kStepK * 2u;  // one operand stage: 256 rows x 64 halves
-
-enum Mode { kGateUp = 0, kDown = 1 };
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 
@@ -239,27 +240,21 @@ __device__ void zero_item(const RoutedGemm& g, const Unit& u, uint32_t ct, const
     }
 }
 
-// DENSE: the rows are the n_entries activation rows themselves (the shared expert), in units
-// of 256 consecutive rows; the weights are dw0/dw1 and the down output row is the unit row.
-template <class Prod, int MODE, bool DENSE>
-__global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, const uint8_t* dw0, const uint8_t* dw1,
-                                                                 uint32_t n_ct) {
-    __shared__ __attribute__((aligned(1024))) uint8_t s_a[2][kStageBytes];
-    __shared__ __attribute__((aligned(1024))) uint8_t s_b[2][kStageBytes];
-    __shared__ uint32_t s_pref[513];  // exclusive prefix of units over groups
-    __shared__ uint32_t s_wsum[8];
-    __shared__ uint32_t s_flag;
-    __shared__ int32_t s_dst[kUnitRows];
-    constexpr int SB = Prod::kSlab;
+// LDS of the wide phase of the routed stage kernel: double-buffered activation and
+// decoded-weight stages and the unit's destination rows (down).
+struct WideSmem {
+    int32_t s_dst[kUnitRows];
+    uint8_t s_a[2][kStageBytes] __attribute__((aligned(1024)));
+    uint8_t s_b[2][kStageBytes] __attribute__((aligned(1024)));
+};
+
+// Unit enumeration (512 threads, once per workgroup): groups with >= wide_min entries,
+// ceil(size / 256) units each; s_pref[gi] = units of the groups before gi, s_pref[512] = all.
+// Returns the status word read at start (bit 1: invalid plan or permutation).
+__device__ __forceinline__ uint32_t scan_wide_units(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const Plan* p = g.plan;
-
-    // ---- unit enumeration: groups with >= wide_min entries, ceil(size / 256) units each ----
-    uint32_t U;
-    if (DENSE) {
-        U = (g.n_entries + kUnitRows - 1u) / kUnitRows;
-    } else {
-    if (tid == 0) s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t ng = p->n_groups < 512u ? p->n_groups : 512u;
     uint32_t units = 0;
     if (tid < ng) {
@@ -281,10 +276,19 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, c
     s_pref[tid + 1] = base + incl;
     if (tid == 0) s_pref[0] = 0;
     __syncthreads();
-    // An invalid plan or permutation: the 64-row tile kernel zeroes every slot.
-    if (s_flag & 2u) return;
-    U = s_pref[512];
-    }
+    return *s_flag;
+}
+
+// The workgroup's share of the U units' items (unit x column tile). DENSE: the rows are the
+// n_entries activation rows themselves (the shared expert), in units of 256 consecutive rows;
+// the weights are dw0/dw1 and the down output row is the unit row.
+template <class Prod, int MODE, bool DENSE>
+__device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* dw0, const uint8_t* dw1, uint32_t n_ct, uint32_t U,
+                           const uint32_t* s_pref, uint8_t (&s_a)[2][kStageBytes], uint8_t (&s_b)[2][kStageBytes],
+                           int32_t* s_dst) {
+    constexpr int SB = Prod::kSlab;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const Plan* p = g.plan;
 
     // ---- per-thread constant roles ----
     const uint32_t wave_u = uint32_t(__builtin_amdgcn_readfirstlane(int(wave)));
@@ -461,29 +465,81 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, c
         wait_barrier();  // the repeated copies of the last step have landed
 
         // ---- epilogue: lane holds column (lane & 31) of each 32-column block, rows
-        // 32 rb + 8 (i / 4) + 4 (lane / 32) + i % 4 of the wave's 128 ----
+        // 32 rb + 8 (i / 4) + 4 (lane / 32) + i % 4 of the wave's 128. Full units (the common
+        // case) store without row checks; the down stage ORs its destination checks over the
+        // item and reports a bad destination (status bit 1) once. ----
+        const uint64_t n_out = g.n_out;
+        const uint32_t col0 = MODE == kGateUp ? 128u * ct + 32u * cq + r32 : 256u * ct + 64u * cq + r32;
+        bool any_bad = false;
+        auto store_rows = [&](auto full_c) {
+            constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+            for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t r = 128u * rh + 32u * uint32_t(rb) + 8u * uint32_t(i >> 2) + 4u * kh + uint32_t(i & 3);
-                if (r >= nrows) continue;
-                const uint32_t a = u.a0 + r;
-                if (MODE == kGateUp) {
-                    g.out_h[uint64_t(a) * g.n_out + 128u * ct + 32u * cq + r32] =
-                        half_sat(silu_fast(acc[rb][0][i]) * acc[rb][1][i]);
-                } else {
-                    const uint32_t d = DENSE ? a : uint32_t(s_dst[r]);
-                    const bool good = DENSE || d < g.n_entries;
-                    if (!good) atomicOr(g.status, 2u);
-                    const uint64_t row = good ? d : a;
-#pragma unroll
-                    for (int cb = 0; cb < 2; ++cb)
-                        g.out_f[row * g.n_out + 256u * ct + 64u * cq + 32u * uint32_t(cb) + r32] =
-                            good ? acc[rb][cb][i] : 0.0f;
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t r = 128u * rh + 32u * uint32_t(rb) + 8u * uint32_t(i >> 2) + 4u * kh + uint32_t(i & 3);
+                    if (!FULL && r >= nrows) continue;
+                    const uint32_t a = u.a0 + r;
+                    if (MODE == kGateUp) {
+                        g.out_h[uint64_t(a) * n_out + col0] = half_sat(silu_fast(acc[rb][0][i]) * acc[rb][1][i]);
+                    } else {
+                        const uint32_t d = DENSE ? a : uint32_t(s_dst[r]);
+                        const bool good = DENSE || d < g.n_entries;
+                        any_bad = any_bad || !good;
+                        float* out = g.out_f + uint64_t(good ? d : a) * n_out + col0;
+                        out[0] = good ? acc[rb][0][i] : 0.0f;
+                        out[32] = good ? acc[rb][1][i] : 0.0f;
+                    }
                 }
-            }
+        };
+        if (nrows == kUnitRows) store_rows(std::true_type());  // workgroup-uniform
+        else store_rows(std::false_type());
+        if (!DENSE && MODE == kDown && any_bad) atomicOr(g.status, 2u);
     }
+}
+
+template <class Prod, int MODE, bool DENSE>
+__global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, const uint8_t* dw0, const uint8_t* dw1,
+                                                                 uint32_t n_ct) {
+    __shared__ __attribute__((aligned(1024))) uint8_t s_a[2][kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_b[2][kStageBytes];
+    __shared__ uint32_t s_pref[513], s_wsum[8], s_flag;
+    __shared__ int32_t s_dst[kUnitRows];
+    uint32_t U;
+    if (DENSE) {
+        U = (g.n_entries + kUnitRows - 1u) / kUnitRows;
+    } else {
+        // An invalid plan or permutation: the 64-row tile kernel zeroes every slot.
+        if (scan_wide_units(g, s_pref, s_wsum, &s_flag) & 2u) return;
+        U = s_pref[512];
+    }
+    wide_items<Prod, MODE, DENSE>(g, dw0, dw1, n_ct, U, s_pref, s_a, s_b, s_dst);
+}
+
+// A whole routed stage in one launch. Each workgroup first takes its share of the wide units'
+// items (as the wide kernel), then draws 64-row tile items of the smaller groups from the
+// per-XCD counters, so workgroups with one wide item fewer take more tiles and the tiles fill
+// the wide units' last round. Without wide units the tiles are taken in the static order.
+template <class Prod, class Frag, int MODE, bool RESIDENT>
+__global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g, uint32_t n_ct, uint32_t n_ntiles,
+                                                                    uint32_t npi, uint32_t n_chunks) {
+    static_assert(kWideThreads == kV2Threads, "one workgroup shape for both phases");
+    __shared__ union Smem {
+        WideSmem w;
+        TileSmem<Frag, 2> t;
+    } sm;
+    __shared__ uint32_t s_pref_w[513], s_pref_t[513], s_wsum[8], s_flag;
+    const uint32_t flag = scan_wide_units(g, s_pref_w, s_wsum, &s_flag);
+    scan_small_tiles(g, s_pref_t, s_wsum, &s_flag);
+    if (flag & 2u) {
+        zero_tile_slots<MODE, 2>(g, n_ntiles, npi, n_chunks);
+        return;
+    }
+    const uint32_t U = s_pref_w[512];
+    wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
+    __syncthreads();  // the wide phase's LDS is free
+    if (U > 0u) tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+    else tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
 }
 
 uint32_t wide_cus() {
@@ -516,6 +572,20 @@ hipError_t launch_wide_t(const RoutedGemm& g, hipStream_t s) {
     // at least wide_min entries, wide_min >= 128), so small layers launch fewer workgroups.
     const uint32_t blocks = wide_blocks(uint64_t(g.n_entries / g.wide_min + 1u) * n_ct);
     wide_gemm_kernel<Prod, MODE, false><<<blocks, kWideThreads, 0, s>>>(g, nullptr, nullptr, n_ct);
+    return hipGetLastError();
+}
+
+template <class Prod, class Frag, int MODE>
+hipError_t launch_stage_t(const RoutedGemm& g, hipStream_t s) {
+    const uint32_t n_ct = MODE == kGateUp ? g.n_out / 128u : g.n_out / 256u;
+    const TilePlan tp = tile_plan<MODE, 2>(g.k, g.n_out);
+    const uint32_t blocks = wide_blocks(uint64_t(g.tile_capacity) * tp.n_chunks);
+    if (tp.resident)
+        routed_stage_kernel<Prod, Frag, MODE, true><<<blocks, kWideThreads, 0, s>>>(g, n_ct, tp.n_ntiles, tp.npi,
+                                                                                   tp.n_chunks);
+    else
+        routed_stage_kernel<Prod, Frag, MODE, false><<<blocks, kWideThreads, 0, s>>>(g, n_ct, tp.n_ntiles, tp.npi,
+                                                                                    tp.n_chunks);
     return hipGetLastError();
 }
 
@@ -554,6 +624,16 @@ hipError_t launch_wide_dense(Fmt fmt, bool gate_up, const DenseGemm& d, hipStrea
     switch (fmt) {
         case Fmt::F16: return gate_up ? launch_dense_t<ProdF16, kGateUp>(d, s) : launch_dense_t<ProdF16, kDown>(d, s);
         case Fmt::BF16: return gate_up ? launch_dense_t<ProdBF16, kGateUp>(d, s) : launch_dense_t<ProdBF16, kDown>(d, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_stage(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s) {
+    if (!gate_up) return hipErrorInvalidValue;  // down runs as two launches (see launch_routed)
+    switch (fmt) {
+        case Fmt::Q8_0: return launch_stage_t<ProdQ80, FragQ80, kGateUp>(g, s);
+        case Fmt::Q4_K: return launch_stage_t<ProdQ4K, FragQ4K, kGateUp>(g, s);
+        case Fmt::Q2_K: return launch_stage_t<ProdQ2K, FragQ2K, kGateUp>(g, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,7 +1,8 @@
 """GPU: the wide routed kernel (256-row units for groups of >= 128 entries).
 
 Groups of at least 128 entries run on the wide kernel, smaller ones on the 64-row tile
-kernels, so a skewed routing exercises both in one stage. Each case checks the expert
+kernels (gate/up: both in one launch, the tiles drawn after the wide units), so a skewed
+routing exercises both in one stage. Each case checks the expert
 stages and the full layer against the CPU oracle with the same bars as the benchmark
 configurations (gate/up within 1 F16 ulp, down parts within 1e-4, layer max-abs 2e-2 and
 rel-L2 5e-3), over every weight format on both stages, with partial last units; and the
@@ -93,6 +94,36 @@ def test_wide_null_address_zeroes_group(moe, layer, orc, gpu_ctx, stream):
     mine[dst[a0:a1]] = True
     assert (parts[mine] == 0).all()
     assert np.isfinite(parts[~mine]).all()
+
+
+def test_small_group_null_address_beside_wide_units(moe, layer, orc, gpu_ctx, stream):
+    # gate/up runs wide units and small-group tiles in one launch; a small group without up
+    # weights zeroes its rows and sets status bit 0 while every other row is computed.
+    print("case null address of a small group beside wide units", flush=True)
+    cfg = _skewed(layer, moe, moe.Q4_K, moe.Q8_0)
+    inp = layer.make_inputs(cfg)
+    ws = layer.LayerWorkspace(gpu_ctx, cfg, inp)
+    ws.run_layer(stream)
+    assert ws.read_status(stream) == (0, 0, 0)
+    E, I, N = cfg.n_experts, cfg.expert_ff, cfg.entries
+    ref = gu.host(ws.hidden, np.uint16).reshape(N, I).copy()
+    counts = np.bincount(gu.host(ws.ids, np.int32), minlength=E)
+    assert counts.max() >= 256
+    small = np.flatnonzero((counts > 0) & (counts < 128))
+    victim = int(small[np.argmax(counts[small])])
+    a0, a1 = _victim_rows(orc, ws, cfg, victim)
+    addr = list(ws.addresses)
+    addr[3 * victim + 1] = 0
+    table = moe.ExpertTable(addr, ws.snap_gu.view(), [ws.w_gate.view(), ws.w_up.view()])
+    gub = moe.GateUpBuffers(table.struct, ws.xs.view(), ws.plan.view(), ws.tiles.view(), ws.hidden.view(),
+                            ws.status.view(0, 4))
+    ws.hidden.tensor.fill_(0x7C01)
+    gu.run(gpu_ctx, stream, lambda s: s.encode_prefill_moe_gu(cfg.shape(), cfg.gate_up_fmt, gub))
+    _, st_gu, _ = ws.read_status(stream)
+    assert st_gu == 1
+    eh = gu.host(ws.hidden, np.uint16).reshape(N, I)
+    assert (eh[a0:a1] == 0).all()
+    assert np.array_equal(eh[:a0], ref[:a0]) and np.array_equal(eh[a1:], ref[a1:])
 
 
 def test_wide_broken_destination_zeroes_parts(moe, layer, orc, gpu_ctx, stream):
