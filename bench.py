@@ -149,7 +149,10 @@ def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: boo
         log(f"stages (us): { {k: round(v * 1e3, 2) for k, v in stages.items()} }")
     gu_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, gub), "gate/up tiles")
     dn_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_down(ws.shape, cfg.down_fmt, dnb), "down tiles")
-    log(f"kernels (us): gate/up tiles {gu_kernel_ms * 1e3:.1f}, down tiles {dn_kernel_ms * 1e3:.1f}")
+    ga_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_grouping(ws.shape, ws.grouping_buffers()), "gather")
+    co_kernel_ms = launch_ms(lambda s: s.encode_prefill_moe_combine(ws.shape, cob), "combine")
+    log(f"kernels (us): gate/up tiles {gu_kernel_ms * 1e3:.1f}, down tiles {dn_kernel_ms * 1e3:.1f}, "
+        f"gather {ga_kernel_ms * 1e3:.1f}, combine {co_kernel_ms * 1e3:.1f}")
 
     plan = ws.plan.tensor.cpu().numpy().view(np.uint32)
     n_groups = int(plan[0])
@@ -157,7 +160,8 @@ def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: boo
     dn_row = moe.row_bytes(cfg.down_fmt, I)
     return {
         "cfg": cfg, "inp": inp, "ms_per_step": ms_per_step, "value": value, "stages": stages,
-        "gu_kernel_ms": gu_kernel_ms, "dn_kernel_ms": dn_kernel_ms,
+        "gu_kernel_ms": gu_kernel_ms, "dn_kernel_ms": dn_kernel_ms, "ga_kernel_ms": ga_kernel_ms,
+        "co_kernel_ms": co_kernel_ms,
         "gu_bytes": n_groups * 2 * I * gu_row + N * d * 2 + N * I * 2, "gu_flops": 2.0 * N * 2 * I * d,
         "dn_bytes": n_groups * d * dn_row + N * I * 2 + N * d * 4, "dn_flops": 2.0 * N * d * I,
     }
@@ -212,9 +216,9 @@ def main() -> int:
         roof = {"bound": "mfma", "achieved": round(gu_tflops, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(gu_tflops / F16_MFMA_PEAK_TFLOPS, 4)}
     fmt_tag = moe.FORMAT_NAMES[cfg.gate_up_fmt].replace('_', '')
-    # The stage is two launches: the wide kernel (groups >= 128 entries) and the 64-row tile
-    # kernel; kernel_us, traffic and the algorithmic bytes all cover both.
-    kernel = f"gate/up stage: routed_gemm_staged_kernel<Frag{fmt_tag}> + wide_gemm_kernel<Prod{fmt_tag}>"
+    # The stage is one launch of the routed stage kernel: 256-row units of the groups with >= 128
+    # entries, then the 64-row tiles of the others (configuration 2 has only the latter).
+    kernel = f"gate/up stage: routed_stage_kernel<Prod{fmt_tag}, Frag{fmt_tag}>"
     roof.update({"kernel": kernel, "kernel_us": round(gu_kernel_ms * 1e3, 2),
                  "traffic": traffic_bytes(args.config, "gate_up"),
                  "algorithmic_bytes": gu_bytes, "algorithmic_flops": gu_flops,
@@ -226,6 +230,13 @@ def main() -> int:
             "grouping_gather": round(gather_bytes / (stages["grouping_gather"] / 1e3) / 1e9, 1),
             "combine": round(comb_bytes / (stages["combine"] / 1e3) / 1e9, 1),
         },
+        # the two HBM kernels alone (HIP events around each launch), against the 8 TB/s peak
+        "gather_kernel": {"kernel_us": round(m["ga_kernel_ms"] * 1e3, 2),
+                          "gbs": round(gather_bytes / (m["ga_kernel_ms"] / 1e3) / 1e9, 1),
+                          "frac": round(gather_bytes / (m["ga_kernel_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "combine_kernel": {"kernel_us": round(m["co_kernel_ms"] * 1e3, 2),
+                           "gbs": round(comb_bytes / (m["co_kernel_ms"] / 1e3) / 1e9, 1),
+                           "frac": round(comb_bytes / (m["co_kernel_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)},
         "down": {"kernel_us": round(dn_kernel_ms * 1e3, 2), "gbs": round(dn_bytes / (dn_kernel_ms / 1e3) / 1e9, 1),
                  "tflops": round(2.0 * N * d * I / (dn_kernel_ms / 1e3) / 1e12, 1),
                  "traffic": traffic_bytes(args.config, "down")},
