@@ -23,17 +23,17 @@ def _cases(layer, moe):
     C = layer.LayerConfig
     return {
         # gate/up Q4_K: 5 slabs; down Q4_K: 2 slabs (resident), 5 column tiles of 256
-        "q4k_npi2": C("stream_q4k", 256, 1280, 24, 3, 512, 0, moe.Q4_K, moe.Q4_K, moe.F16, seed=301),
+        "q4k_5slab": C("tiles_q4k", 256, 1280, 24, 3, 512, 0, moe.Q4_K, moe.Q4_K, moe.F16, seed=301),
         # gate/up Q2_K: 4 slabs; down Q8_0: 4 slabs (streamed), 4 column tiles of 256
-        "q80_npi4": C("stream_q80", 256, 1024, 16, 4, 1024, 0, moe.Q2_K, moe.Q8_0, moe.F16, seed=302),
+        "q2k_q80": C("tiles_q80", 256, 1024, 16, 4, 1024, 0, moe.Q2_K, moe.Q8_0, moe.F16, seed=302),
         # gate/up Q4_K: 1 slab, 4 column tiles of 128; down Q8_0: 2 slabs, 1 column tile
-        "q80_npi2": C("stream_q80b", 128, 256, 8, 2, 512, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=303),
+        "q80_2slab": C("tiles_q80b", 128, 256, 8, 2, 512, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=303),
         # gate/up Q4_K: 3 column tiles; down K = 384 on the plain tile kernel
-        "odd_tiles": C("stream_odd", 192, 512, 12, 2, 384, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=304),
+        "odd_tiles": C("tiles_odd", 192, 512, 12, 2, 384, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=304),
     }
 
 
-@pytest.mark.parametrize("case", ["q4k_npi2", "q80_npi4", "q80_npi2", "odd_tiles"])
+@pytest.mark.parametrize("case", ["q4k_5slab", "q2k_q80", "q80_2slab", "odd_tiles"])
 def test_tile_kernels_layer(moe, layer, orc, gpu_ctx, stream, case):
     cfg = _cases(layer, moe)[case]
     print(f"case tiles {case}: T {cfg.rows} d {cfg.hidden} E {cfg.n_experts} top-{cfg.top_k} "
@@ -51,7 +51,7 @@ def _victim_rows(orc, ws, cfg, victim):
     return int(pf["grp_start"][gi]), int(pf["grp_start"][gi + 1])
 
 
-@pytest.mark.parametrize("case", ["q4k_npi2", "q80_npi4"])
+@pytest.mark.parametrize("case", ["q4k_5slab", "q2k_q80"])
 def test_tile_null_address_zeroes_group(moe, layer, orc, gpu_ctx, stream, case):
     print(f"case tiles null expert address {case}", flush=True)
     cfg = _cases(layer, moe)[case]
@@ -96,7 +96,7 @@ def test_tile_null_address_zeroes_group(moe, layer, orc, gpu_ctx, stream, case):
 
 def test_tile_broken_destination_zeroes_parts(moe, layer, orc, gpu_ctx, stream):
     print("case tiles duplicate destination", flush=True)
-    cfg = _cases(layer, moe)["q80_npi4"]
+    cfg = _cases(layer, moe)["q2k_q80"]
     ws = layer.LayerWorkspace(gpu_ctx, cfg, layer.make_inputs(cfg))
     ws.run_layer(stream)
     dst = gu.host(ws.dst, np.int32).copy()
