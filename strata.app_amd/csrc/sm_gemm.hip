@@ -338,17 +338,13 @@ hipError_t launch_tiles(const RoutedGemm& g, hipStream_t s) {
     return hipGetLastError();
 }
 
-// A stage with wide units. gate/up: one launch of the routed stage kernel (wide units, then
-// the small groups' tiles) where the tiles fit the staged kernel. Down: the wide kernel, then
-// the tile kernel. A down tile item streams a whole expert matrix (8 column tiles) through
-// L2, which evicts the activations that concurrent wide units share across column tiles:
-// with a skewed routing (T = 8192, Zipf 1.1) the single launch measured 460 us against
-// 419 us for the two.
+// A stage with wide units: one launch of the routed stage kernel (wide units and the small
+// groups' tiles) where the tiles fit the staged kernel, else the wide kernel and then the
+// plain tile kernel.
 template <class Frag, int MODE>
 hipError_t launch_routed(Fmt fmt, const RoutedGemm& g, hipStream_t s) {
     if (g.wide_min == ~0u) return launch_tiles<Frag, MODE>(g, s);
-    if (MODE == kGateUp && g.k % kSlab == 0 && g.n_out % Staged<MODE, 2>::kOut == 0)
-        return launch_stage(fmt, true, g, s);
+    if (g.k % kSlab == 0 && g.n_out % Staged<MODE, 2>::kOut == 0) return launch_stage(fmt, MODE == kGateUp, g, s);
     const hipError_t e = launch_wide(fmt, MODE == kGateUp, g, s);
     return e != hipSuccess ? e : launch_tiles<Frag, MODE>(g, s);
 }

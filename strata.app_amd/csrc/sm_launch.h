@@ -97,17 +97,15 @@ struct RoutedGemm {
     uint32_t* counters;         // kCounterWords per-XCD item counters, zeroed by the plan check
 };
 // Groups of at least g.wide_min entries run on the wide kernel, the others on the 64-row
-// tile kernels; gate/up runs both in one launch where they fit (the routed stage kernel):
-// each workgroup takes its wide units first and then draws tiles, so tiles fill the wide
-// units' tail.
+// tile kernels; both run in one launch where they fit (the routed stage kernel).
 hipError_t launch_gate_up(Fmt fmt, const RoutedGemm& g, hipStream_t s);
 hipError_t launch_down(Fmt fmt, const RoutedGemm& g, hipStream_t s);
 // Whether the wide kernel supports a stage: a block format, K a multiple of 64, and whole
 // 256-row column tiles (gate/up: 128 hidden columns, down: 256 output columns).
 bool wide_fits(Fmt fmt, bool gate_up, uint32_t k, uint32_t n_out);
 hipError_t launch_wide(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s);
-// One launch for a whole routed gate/up stage: wide units (groups >= g.wide_min), then the
-// other groups' 64-row tiles in the staged form (K a multiple of 256, whole column tiles).
+// One launch for a whole routed stage: wide units (groups >= g.wide_min) and the other
+// groups' 64-row tiles in the staged form (K a multiple of 256, whole column tiles).
 hipError_t launch_stage(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s);
 constexpr uint32_t kWideMin = 128;
 

@@ -516,10 +516,14 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, c
     wide_items<Prod, MODE, DENSE>(g, dw0, dw1, n_ct, U, s_pref, s_a, s_b, s_dst);
 }
 
-// A whole routed stage in one launch. Each workgroup first takes its share of the wide units'
-// items (as the wide kernel), then draws 64-row tile items of the smaller groups from the
-// per-XCD counters, so workgroups with one wide item fewer take more tiles and the tiles fill
-// the wide units' last round. Without wide units the tiles are taken in the static order.
+// A whole routed stage in one launch. gate/up: each workgroup first takes its share of the
+// wide units' items (as the wide kernel), then draws 64-row tile items of the smaller groups
+// from the per-XCD counters, so workgroups with one wide item fewer take more tiles and the
+// tiles fill the wide units' last round (without wide units the tiles are taken in the static
+// order). Down: the tiles first, in the static order, then the wide units. A down tile item
+// streams its expert's whole weight matrix through L2, which would evict the activation rows
+// that concurrently running wide units share across column tiles; taken first, the tiles
+// overlap the wide units only at the boundary.
 template <class Prod, class Frag, int MODE, bool RESIDENT>
 __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g, uint32_t n_ct, uint32_t n_ntiles,
                                                                     uint32_t npi, uint32_t n_chunks) {
@@ -536,10 +540,16 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
         return;
     }
     const uint32_t U = s_pref_w[512];
-    wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
-    __syncthreads();  // the wide phase's LDS is free
-    if (U > 0u) tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
-    else tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+    if (MODE == kGateUp) {
+        wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
+        __syncthreads();  // the wide phase's LDS is free
+        if (U > 0u) tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+        else tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+    } else {
+        tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+        __syncthreads();  // the tile phase's LDS is free
+        wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
+    }
 }
 
 uint32_t wide_cus() {
@@ -629,11 +639,13 @@ hipError_t launch_wide_dense(Fmt fmt, bool gate_up, const DenseGemm& d, hipStrea
 }
 
 hipError_t launch_stage(Fmt fmt, bool gate_up, const RoutedGemm& g, hipStream_t s) {
-    if (!gate_up) return hipErrorInvalidValue;  // down runs as two launches (see launch_routed)
     switch (fmt) {
-        case Fmt::Q8_0: return launch_stage_t<ProdQ80, FragQ80, kGateUp>(g, s);
-        case Fmt::Q4_K: return launch_stage_t<ProdQ4K, FragQ4K, kGateUp>(g, s);
-        case Fmt::Q2_K: return launch_stage_t<ProdQ2K, FragQ2K, kGateUp>(g, s);
+        case Fmt::Q8_0:
+            return gate_up ? launch_stage_t<ProdQ80, FragQ80, kGateUp>(g, s) : launch_stage_t<ProdQ80, FragQ80, kDown>(g, s);
+        case Fmt::Q4_K:
+            return gate_up ? launch_stage_t<ProdQ4K, FragQ4K, kGateUp>(g, s) : launch_stage_t<ProdQ4K, FragQ4K, kDown>(g, s);
+        case Fmt::Q2_K:
+            return gate_up ? launch_stage_t<ProdQ2K, FragQ2K, kGateUp>(g, s) : launch_stage_t<ProdQ2K, FragQ2K, kDown>(g, s);
         default: return hipErrorInvalidValue;
     }
 }
