@@ -38,10 +38,11 @@ struct sm_context {
     bool ring_claimed[kRingSlots] = {};  // filled by an encode whose segment is not committed yet
     uint32_t ring_next = 0;
     std::mutex ring_mu;
-    // Second stream (default priority) for launches that depend on nothing recorded before
-    // them in their segment (the shared expert of a full layer): they start behind a fork
-    // event recorded on the caller's stream when the segment is committed, and a later step
-    // marked `join` waits for them. side_mu keeps one commit's event records and waits together.
+    // Second stream (default priority) for launches off the critical path of a full layer (the
+    // shared expert): a side launch waits for the latest fork event, recorded on the caller's
+    // stream before a step marked `fork_before` (or, if none came yet, right before the side
+    // launch itself); a later step marked `join` waits for the side launches. side_mu keeps
+    // one commit's event records and waits together.
     hipStream_t side = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     std::mutex side_mu;
@@ -60,8 +61,9 @@ struct sm_segment {
         const char* label;
         std::function<hipError_t(hipStream_t)> run;
         int ring_slot = -1, ring_slot2 = -1;
-        bool side = false;  // runs on the context's side stream (untimed commits)
-        bool join = false;  // waits for every side launch recorded before it
+        bool side = false;         // runs on the context's side stream (untimed commits)
+        bool join = false;         // waits for every side launch recorded before it
+        bool fork_before = false;  // later side launches wait for the steps before this one
     };
     std::vector<Step> steps;
     bool failed = false;
@@ -722,13 +724,14 @@ sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
     bool use_side = false;
     for (const auto& step : seg->steps) use_side = use_side || (step.side && ev == nullptr);
     std::unique_lock<std::mutex> side_lk(ctx->side_mu, std::defer_lock);
-    if (use_side) {
-        side_lk.lock();
-        if (st == SM_OK && (hipEventRecord(ctx->fork_ev, stream) != hipSuccess ||
-                            hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0) != hipSuccess))
-            st = SM_E_DEVICE;
-    }
-    bool side_open = false;  // side launches not yet joined
+    if (use_side) side_lk.lock();
+    bool side_open = false;     // side launches not yet joined
+    bool forked = false;        // the side stream waits for some point of this segment
+    bool fork_pending = false;  // a fork event the next side launch must wait for
+    auto fork = [&]() {
+        if (st == SM_OK && hipEventRecord(ctx->fork_ev, stream) != hipSuccess) st = SM_E_DEVICE;
+        fork_pending = true;
+    };
     auto join = [&]() {
         if (st == SM_OK && (hipEventRecord(ctx->join_ev, ctx->side) != hipSuccess ||
                             hipStreamWaitEvent(stream, ctx->join_ev, 0) != hipSuccess))
@@ -739,7 +742,15 @@ sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
         auto& step = seg->steps[i];
         if (st != SM_OK) break;
         if (step.join && side_open) join();
+        if (use_side && step.fork_before) fork();
         const hipStream_t hs = use_side && step.side ? ctx->side : stream;
+        if (hs != stream) {
+            if (!forked && !fork_pending) fork();
+            if (st == SM_OK && fork_pending && hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0) != hipSuccess)
+                st = SM_E_DEVICE;
+            fork_pending = false;
+            forked = true;
+        }
         side_open = side_open || hs != stream;
         if (st == SM_OK && ev && hipEventRecord(ev[2 * i], hs) != hipSuccess) st = SM_E_DEVICE;
         if (st == SM_OK && step.run(hs) != hipSuccess) st = SM_E_DEVICE;
@@ -1042,7 +1053,11 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
         }
     // The shared expert reads only the activations and its weights, which no earlier launch
     // writes (checked above), so it runs beside routing and the routed experts; combine joins.
+    // The shared expert waits for the work recorded before this layer (in a segment of
+    // several layers, the previous layer), not for this layer's routing.
+    const size_t first = seg->steps.size();
     encode_route_gather_launch(seg, s, rr, ro, gr);
+    seg->steps[first].fork_before = true;
     if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
     if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
     encode_combine_launch(seg, s, co, has_shared);

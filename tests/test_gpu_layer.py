@@ -111,3 +111,33 @@ def test_commit_timed_matches_commit(moe, layer, orc, gpu_ctx, stream):
     assert [label for label, _ in got] == ["gate/up plan validate", "gate/up tiles"]
     assert all(ms > 0 for _, ms in got)
     assert np.array_equal(gu.host(ws.hidden, np.uint16), ref)
+
+
+def test_layer_after_a_producer_in_one_segment(moe, layer, gpu_ctx, stream):
+    """A segment holding a launch that writes the activations and then the full layer: the
+    layer's shared expert (which runs on the context's second stream) sees the written values,
+    so the outputs equal those of the layer committed on its own."""
+    print("case layer behind a producer in one segment", flush=True)
+    cfg = layer.LayerConfig("seg_order", 256, 256, 16, 4, 128, 256, moe.Q4_K, moe.Q8_0, moe.F16, seed=61)
+    ws = layer.LayerWorkspace(gpu_ctx, cfg, layer.make_inputs(cfg))
+    ws.run_layer(stream)
+    assert ws.read_status(stream) == (0, 0, 0)
+    out_ref = gu.host(ws.out, np.float32).copy()
+    sh_ref = gu.host(ws.sh_out, np.float32).copy()
+    T, d = cfg.rows, cfg.hidden
+    x = gu.host(ws.x, np.uint16).reshape(T, d)
+    # F16 "weights" [d rows][T values] whose K-major dequant [T][d] is x itself
+    src = gpu_ctx.register(gu.dev(np.ascontiguousarray(x.T)))
+    ws.x.tensor.fill_(0x7C01)  # poison: only the dequant in the same segment restores x
+    ws.out.tensor.fill_(float("nan"))
+    ws.sh_out.tensor.fill_(float("nan"))
+    seg = gpu_ctx.segment()
+    ok, err = seg.encode_prefill_dequant(moe.F16, d, T, src.view(), ws.x.view())
+    assert ok, err
+    ok, err = seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, ws.layer_buffers())
+    assert ok, err
+    seg.commit(stream)
+    assert ws.read_status(stream) == (0, 0, 0)
+    assert np.array_equal(gu.host(ws.sh_out, np.float32).view(np.uint32), sh_ref.view(np.uint32))
+    assert np.array_equal(gu.host(ws.out, np.float32).view(np.uint32), out_ref.view(np.uint32))
+
