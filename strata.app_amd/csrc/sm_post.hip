@@ -14,7 +14,10 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 
 // out[t,c] = fma(shared[t,c], sigmoid(gl[t]), s) with s = 0 then s = fma(w[t,r], parts[t,r,c], s)
 // for r = 0..k-1 in rank order (prefill_moe.metal:1201-1222): a per-token gather-reduce in a
-// fixed order, no atomics. Each thread owns four consecutive columns of one token.
+// fixed order, no atomics. Each thread owns four consecutive columns of one token. KC > 0: the
+// top-k is KC, and every rank's 16 bytes are loaded before the first fma, so a thread keeps KC
+// loads in flight; KC = 0: any top-k, one rank at a time.
+template <int KC>
 __global__ __launch_bounds__(256) void combine_kernel(const float4v* __restrict__ parts,
                                                       const float* __restrict__ weights,
                                                       const float4v* __restrict__ shared,
@@ -26,13 +29,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const float4v* __restrict_
     const uint32_t t = uint32_t(idx / v4), c = uint32_t(idx % v4);
     float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
     const float4v* prow = parts + uint64_t(t) * K * v4 + c;
-    for (uint32_t r = 0; r < K; ++r) {
-        const float w = weights[uint64_t(t) * K + r];
-        const float4v p = prow[uint64_t(r) * v4];
+    auto add = [&](float w, const float4v& p) {
         s[0] = __builtin_fmaf(w, p[0], s[0]);
         s[1] = __builtin_fmaf(w, p[1], s[1]);
         s[2] = __builtin_fmaf(w, p[2], s[2]);
         s[3] = __builtin_fmaf(w, p[3], s[3]);
+    };
+    if constexpr (KC > 0) {
+        float4v p[KC];
+        float w[KC];
+#pragma unroll
+        for (int r = 0; r < KC; ++r) p[r] = __builtin_nontemporal_load(prow + uint64_t(r) * v4);
+#pragma unroll
+        for (int r = 0; r < KC; ++r) w[r] = weights[uint64_t(t) * KC + r];
+#pragma unroll
+        for (int r = 0; r < KC; ++r) add(w[r], p[r]);
+    } else {
+        for (uint32_t r = 0; r < K; ++r) add(weights[uint64_t(t) * K + r], prow[uint64_t(r) * v4]);
     }
     if (shared != nullptr) {
         const float gate = sigmoid(gl[t]);
@@ -57,9 +70,15 @@ hipError_t launch_combine(const float* parts, const float* weights, const float*
                           float* out, uint32_t rows, uint32_t K, uint32_t d, hipStream_t s) {
     const uint32_t v4 = d / 4;
     const uint64_t blocks = (uint64_t(rows) * v4 + 255) / 256;
-    combine_kernel<<<dim3(uint32_t(blocks)), 256, 0, s>>>(
-        reinterpret_cast<const float4v*>(parts), weights, reinterpret_cast<const float4v*>(shared), gl,
-        reinterpret_cast<float4v*>(out), rows, K, v4);
+    const auto* p = reinterpret_cast<const float4v*>(parts);
+    const auto* sh = reinterpret_cast<const float4v*>(shared);
+    auto* o = reinterpret_cast<float4v*>(out);
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    switch (K) {  // the benchmark layers' top-k values
+        case 8: combine_kernel<8><<<grid, 256, 0, s>>>(p, weights, sh, gl, o, rows, K, v4); break;
+        case 10: combine_kernel<10><<<grid, 256, 0, s>>>(p, weights, sh, gl, o, rows, K, v4); break;
+        default: combine_kernel<0><<<grid, 256, 0, s>>>(p, weights, sh, gl, o, rows, K, v4); break;
+    }
     return hipGetLastError();
 }
 
