@@ -185,8 +185,18 @@ struct FragQ80 {
     template <class M = FromGlobal>
     __device__ __forceinline__ void load(const uint8_t* slab, int g) {
         const uint8_t* p = slab + 68 * g;
+        if constexpr (__is_same(M, FromGlobal)) {  // four dword-aligned 16-byte loads and a dword
 #pragma unroll
-        for (int i = 0; i < 17; ++i) w[i] = M::template ld<uint32_t>(p + 4 * i);
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 v = M::template ld<u32x4>(p + 16 * i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
+            }
+            w[16] = M::template ld<uint32_t>(p + 64);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 17; ++i) w[i] = M::template ld<uint32_t>(p + 4 * i);
+        }
     }
     __device__ __forceinline__ void prepare() {}
     // Block b (0/1) occupies bytes 34b .. 34b+33 of the 68: d at 34b, q at 34b+2.

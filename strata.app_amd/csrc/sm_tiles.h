@@ -302,6 +302,15 @@ struct TileSmem {
     uint32_t s_next;
 };
 
+// Weights straight to registers instead of through an LDS image: where only one image would
+// fit beside the resident activation tile (Q8_0 down, K <= 512), each lane loads its own
+// fragments for the next step while it multiplies the current one, so the weight stream
+// never waits for a barrier. (For the other formats and shapes the LDS image measured faster.)
+template <class Frag, int MODE, bool RESIDENT>
+struct DirectWeights {
+    static constexpr bool value = MODE == kDown && RESIDENT && StagedBuffers<Frag, 2>::kWBuf == 1;
+};
+
 // Launch shape of the staged tile kernels for one stage: column tiles of 128*NF weight rows,
 // `npi` of them per item (about 8 (column tile, slab) steps per item; with the activation tile
 // resident (K <= 512) every column tile of a row tile goes to one item, so the tile is read
@@ -393,6 +402,55 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
     };
     if (RESIDENT)
         for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
+    constexpr bool DIRECT = DirectWeights<Frag, MODE, RESIDENT>::value;
+    if constexpr (DIRECT) {
+        // This lane's fragments of `step`, from global memory.
+        auto load_frags = [&](Frag (&c)[NF], uint32_t step) {
+            const uint32_t nt = t.nt_begin + step / n_slabs, sb = step % n_slabs;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const uint32_t r = nt * S::kImageRows + S::image_row(wave, n, f);
+                c[f].template load<FromGlobal>(t.w0 + uint64_t(r) * g.row_bytes + uint64_t(sb) * SB, gq);
+            }
+        };
+        auto run_direct = [&](auto rb_const) {
+            constexpr int RB = decltype(rb_const)::value;
+            float4v acc[NF][4];
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
+            Frag fa[NF], fb[NF];
+            load_frags(fa, 0);
+            // Steps in pairs, so the two fragment sets alternate without copies.
+            auto do_step = [&](uint32_t step, Frag (&cur)[NF], Frag (&nxt)[NF]) {
+                // The resident slabs (first step) and this step's fragments.
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                if (step == 0) __syncthreads();
+                load_frags(nxt, step + 1 < n_steps ? step + 1 : step);
+#pragma unroll
+                for (int f = 0; f < NF; ++f) cur[f].prepare();
+                const uint32_t sb = step % n_slabs;
+                slab_mma<Frag, NF, RB>(sa[sb], n, gq, cur, acc, [](int) {});
+                if (sb == n_slabs - 1u)
+                    staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, (t.nt_begin + step / n_slabs) * S::kOut, wave, n,
+                                                  gq, acc);
+            };
+            for (uint32_t step = 0; step < n_steps; step += 2) {
+                do_step(step, fa, fb);
+                if (step + 1 < n_steps) do_step(step + 1, fb, fa);
+            }
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated last fragment loads
+        };
+        switch ((t.a1 - t.a0 + 15u) / 16u) {  // workgroup-uniform
+            case 1: run_direct(std::integral_constant<int, 1>()); break;
+            case 2: run_direct(std::integral_constant<int, 2>()); break;
+            case 3: run_direct(std::integral_constant<int, 3>()); break;
+            default: run_direct(std::integral_constant<int, 4>()); break;
+        }
+        if (dynamic && threadIdx.x == 0) sm.s_next = x * per + next;
+        continue;
+    }
 #pragma unroll
     for (int p = 0; p < 8; ++p) issue_part(0, p);
     // The step loop, specialised on the number of 16-row blocks holding entries.
