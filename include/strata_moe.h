@@ -141,7 +141,7 @@ typedef struct sm_grouping_buffers {
     sm_view ids;              /* I32 [T*k] route ids, token-major                         */
     sm_view mixed_h;          /* F16 [T,d], 16-byte aligned                               */
     sm_view histogram;        /* U32 [ceil(T*k/256) + 1][E]: tile cursors + first slots   */
-    sm_view plan;             /* 6400-byte PfPlan slot (the tail holds stage counters)   */
+    sm_view plan;             /* 6400-byte PfPlan slot (tail: stage counters, arrival) */
     sm_view tiles;            /* U32x2 [ceil(T*k/64)+E] {group, first_entry}              */
     sm_view source_rows;      /* I32 [T*k]: grouped entry -> token                        */
     sm_view destination_rows; /* I32 [T*k]: grouped entry -> route index t*k+r            */

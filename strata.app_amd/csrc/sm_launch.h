@@ -27,6 +27,10 @@ constexpr uint32_t kCounterBytes = 6208;
 constexpr uint32_t kCounterWords = 8;
 static_assert(sizeof(Plan) <= kCounterBytes && kCounterBytes + 2 * 4 * kCounterWords <= kPlanSlotBytes,
               "counters in the plan slot's padding");
+// The grouping's column-scan workgroups count themselves in at this word of the slot (the
+// count kernel zeroes it; the plan fill that follows leaves it zero).
+constexpr uint32_t kArriveBytes = kCounterBytes + 2 * 4 * kCounterWords;
+static_assert(kArriveBytes + 4 <= kPlanSlotBytes, "arrival word inside the plan slot");
 
 enum class Fmt : int { Q8_0 = 1, Q4_K = 2, Q2_K = 3, F16 = 4, BF16 = 5 };
 
@@ -40,9 +44,17 @@ hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, 
 // ---- grouping ----
 // hist has ceil(N/256) + 1 rows of n_experts u32; the extra last row holds each expert's
 // first grouped slot.
+// Full-layer duties of the grouping's scan workgroup: the expert stages' status words and the
+// destination bitset are zeroed before the gather's checks (launch_gather_checked) run.
+struct GroupPrep {
+    uint32_t* status = nullptr;
+    uint32_t* status2 = nullptr;
+    uint32_t* clear = nullptr;
+    uint32_t clear_words = 0;
+};
 hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
                            uint32_t* hist, Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst,
-                           hipStream_t s);
+                           const GroupPrep* prep, hipStream_t s);
 hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
                          const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
 
@@ -70,6 +82,14 @@ struct PlanCheck {
     uint32_t n_counters;
 };
 hipError_t launch_plan_validate(const PlanCheck& c, hipStream_t s);
+// The gather of a full layer with both expert stages' checks in the same launch: one extra
+// workgroup runs the plan check `c` (its `clear` and status clearing are not used: the
+// grouping's GroupPrep zeroed both status words and the bitset `bits`), and every gather
+// workgroup marks eight entries of `dst` in `bits`, setting bit 1 of `c.status2` for an entry
+// outside [0, n_entries) or a repeated one.
+hipError_t launch_gather_checked(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
+                                 const Plan* plan, uint32_t n_entries, _Float16* xs, const PlanCheck& c,
+                                 const int32_t* dst, uint32_t* bits, hipStream_t s);
 // Checks that `dst` is a permutation of [0, n_entries) with a bitset (zeroed first unless
 // `bitset_clear` is false because a PlanCheck cleared it).
 hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bitset, uint32_t* status,

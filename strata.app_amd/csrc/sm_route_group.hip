@@ -196,19 +196,21 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 // ---------------------------------------------------------------------------------------
 // Grouping. Results equal a stable counting sort of the valid entries by expert id:
 //   count   one 256-entry tile per workgroup, LDS histogram, raw counts to hist[tile][e]
-//   colscan per expert column, exclusive prefix over tiles (32 tile slices per column in
-//           parallel); column totals to the extra row hist[n_tiles][e]
-//   plan    one workgroup: block scans over experts give each expert's first slot, group
-//           index and first tile; writes the PfPlan slot and the 64-entry tile list, and
-//           replaces hist[n_tiles][e] by the expert's first slot
+//   scan    per expert column, exclusive prefix over tiles (32 tile slices per column in
+//           parallel); then the last workgroup to finish: block scans over experts give
+//           each expert's first slot, group index and first tile; writes the PfPlan slot
+//           and the 64-entry tile list, and the expert's first slot to the extra row
+//           hist[n_tiles][e]
 //   scatter one 256-entry tile per workgroup: hist row += first slot (the reference's
 //           "cursor at tile start"); stable in-tile rank from per-wave ballot matching of
 //           the 9-bit ids plus the counts of earlier waves; src[slot] = i/k, dst[slot] = i
 // ---------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void group_count_kernel(const int32_t* __restrict__ ids, uint32_t N,
-                                                          uint32_t E, uint32_t* __restrict__ hist) {
+                                                          uint32_t E, uint32_t* __restrict__ hist,
+                                                          uint32_t* __restrict__ arrive) {
     __shared__ uint32_t cnt[512];
     const uint32_t tile = blockIdx.x, tid = threadIdx.x;
+    if (tile == 0 && tid == 0) *arrive = 0u;
     for (uint32_t e = tid; e < E; e += 256) cnt[e] = 0;
     __syncthreads();
     const uint64_t entry = uint64_t(tile) * kCountTile + tid;
@@ -220,33 +222,10 @@ __global__ __launch_bounds__(256) void group_count_kernel(const int32_t* __restr
     for (uint32_t e = tid; e < E; e += 256) hist[uint64_t(tile) * E + e] = cnt[e];
 }
 
-__global__ __launch_bounds__(1024) void group_colscan_kernel(uint32_t* __restrict__ hist, uint32_t E,
-                                                             uint32_t n_tiles) {
-    __shared__ uint32_t part[32][33];
-    const uint32_t el = threadIdx.x & 31u, slice = threadIdx.x >> 5;
-    const uint32_t e = blockIdx.x * 32u + el;
-    const uint32_t per = (n_tiles + 31u) / 32u;
-    const uint32_t t_begin = slice * per;
-    const uint32_t t_end = t_begin + per < n_tiles ? t_begin + per : n_tiles;
-    uint32_t local = 0;
-    if (e < E)
-        for (uint32_t t = t_begin; t < t_end; ++t) local += hist[uint64_t(t) * E + e];
-    part[slice][el] = local;
-    __syncthreads();
-    uint32_t run = 0;
-    for (uint32_t s = 0; s < slice; ++s) run += part[s][el];
-    if (e >= E) return;
-    if (slice == 31u) hist[uint64_t(n_tiles) * E + e] = run + local;
-    for (uint32_t t = t_begin; t < t_end; ++t) {
-        const uint64_t h = uint64_t(t) * E + e;
-        const uint32_t c = hist[h];
-        hist[h] = run;
-        run += c;
-    }
-}
-
-// Exclusive scan over the 512 threads of a workgroup; returns the prefix and the total.
-__device__ __forceinline__ uint32_t block_scan_512(uint32_t v, uint32_t* wave_tot, uint32_t& total) {
+// Exclusive scan over the NT threads of a workgroup; returns the prefix and the total.
+template <uint32_t NT>
+__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* wave_tot, uint32_t& total) {
+    constexpr uint32_t kWaves = NT / 64;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     uint32_t inc = v;
 #pragma unroll
@@ -257,7 +236,8 @@ __device__ __forceinline__ uint32_t block_scan_512(uint32_t v, uint32_t* wave_to
     if (lane == 63u) wave_tot[wave] = inc;
     __syncthreads();
     uint32_t before = 0, all = 0;
-    for (uint32_t w = 0; w < 8; ++w) {
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) {
         if (w < wave) before += wave_tot[w];
         all += wave_tot[w];
     }
@@ -266,36 +246,95 @@ __device__ __forceinline__ uint32_t block_scan_512(uint32_t v, uint32_t* wave_to
     return before + inc - v;
 }
 
-__global__ __launch_bounds__(512) void group_plan_kernel(uint32_t* __restrict__ hist, uint32_t E, uint32_t N,
-                                                         uint32_t n_tiles, Plan* __restrict__ plan,
-                                                         uint32_t* __restrict__ tiles) {
-    __shared__ uint32_t wave_tot[8];
-    const uint32_t e = threadIdx.x;
-    const uint32_t count = e < E ? hist[uint64_t(n_tiles) * E + e] : 0u;
+// Column scan, then the plan. Workgroup c scans expert columns [32c, 32c + 32): thread
+// (slice, e) takes a contiguous run of tiles, the slice partials give each run's exclusive
+// start, each run is rewritten in place with its column prefix, and the column total goes to
+// the extra row hist[n_tiles][e] (a device-coherent store, waited for). Each workgroup then
+// counts itself in at `arrive` (zeroed by the count kernel, which runs just before), and the
+// last to arrive reads the totals with device-coherent loads and builds the plan: block
+// scans over the experts give each expert's first slot, group index and first tile; the slot
+// is filled, the group fields written, tile i finds its group by binary search over the
+// groups' first tiles (no serial per-expert loop), and hist[n_tiles][e] becomes the expert's
+// first slot. `prep` (a full layer) zeroes the two stage status words and the destination
+// bitset that the gather's checks use.
+constexpr uint32_t kScanThreads = 1024;
+__global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t* __restrict__ hist, uint32_t E,
+                                                                       uint32_t N, uint32_t n_tiles,
+                                                                       Plan* __restrict__ plan,
+                                                                       uint32_t* __restrict__ tiles,
+                                                                       uint32_t* __restrict__ arrive, GroupPrep prep) {
+    __shared__ uint32_t part[32][33];
+    __shared__ uint32_t wave_tot[kScanThreads / 64];
+    __shared__ uint32_t s_tstart[512], s_first[512], s_last;
+    const uint32_t tid = threadIdx.x;
+    if (blockIdx.x == 0 && tid == 0) {
+        if (prep.status != nullptr) *prep.status = 0u;
+        if (prep.status2 != nullptr) *prep.status2 = 0u;
+    }
+    for (uint32_t i = blockIdx.x * kScanThreads + tid; i < prep.clear_words; i += gridDim.x * kScanThreads)
+        prep.clear[i] = 0u;
+    {
+        const uint32_t el = tid & 31u, slice = tid >> 5;
+        const uint32_t e = blockIdx.x * 32u + el;
+        const uint32_t per = (n_tiles + 31u) / 32u;
+        const uint32_t t_begin = slice * per < n_tiles ? slice * per : n_tiles;
+        const uint32_t t_end = t_begin + per < n_tiles ? t_begin + per : n_tiles;
+        uint32_t local = 0;
+        if (e < E)
+            for (uint32_t t = t_begin; t < t_end; ++t) local += hist[uint64_t(t) * E + e];
+        part[slice][el] = local;
+        __syncthreads();
+        if (e < E) {
+            uint32_t run = 0;
+            for (uint32_t sl = 0; sl < slice; ++sl) run += part[sl][el];
+            // The total is the only value another workgroup reads in this launch: a
+            // device-coherent store (no L2-wide write-back needed).
+            if (slice == 31u)
+                __hip_atomic_store(&hist[uint64_t(n_tiles) * E + e], run + local, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t t = t_begin; t < t_end; ++t) {
+                const uint64_t h = uint64_t(t) * E + e;
+                const uint32_t c = hist[h];
+                hist[h] = run;
+                run += c;
+            }
+        }
+    }
+    // Count in once this workgroup's totals are stored; the last to arrive reads all totals
+    // with device-coherent loads. The rewritten rows are read only by the scatter launch.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(arrive, 1u) == gridDim.x - 1u ? 1u : 0u;
+    __syncthreads();
+    if (!s_last) return;
+
+    const uint32_t count =
+        tid < E ? __hip_atomic_load(&hist[uint64_t(n_tiles) * E + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                : 0u;
     uint32_t total_count, total_groups, total_tiles;
-    const uint32_t first = block_scan_512(count, wave_tot, total_count);
-    const uint32_t grp = block_scan_512(count ? 1u : 0u, wave_tot, total_groups);
+    const uint32_t first = block_scan<kScanThreads>(count, wave_tot, total_count);
+    const uint32_t grp = block_scan<kScanThreads>(count ? 1u : 0u, wave_tot, total_groups);
     const uint32_t ntile_e = (count + kExpertTile - 1) / kExpertTile;
-    const uint32_t tstart = block_scan_512(ntile_e, wave_tot, total_tiles);
+    const uint32_t tstart = block_scan<kScanThreads>(ntile_e, wave_tot, total_tiles);
     // Whole 6400-byte slot: every word defined (unused group slots -1 / 0, tail zero).
     uint32_t* words = reinterpret_cast<uint32_t*>(plan);
-    for (uint32_t i = e; i < kPlanSlotBytes / 4; i += 512) {
+    for (uint32_t i = tid; i < kPlanSlotBytes / 4; i += kScanThreads) {
         uint32_t val = 0;
         if (i >= 8 && i < 8 + 1024) val = 0xffffffffu;  // grp_e[], grp_res[] = -1
         words[i] = val;
     }
+    if (count) {
+        s_tstart[grp] = tstart;
+        s_first[grp] = first;
+    }
     __syncthreads();
     if (count) {
-        plan->grp_e[grp] = int32_t(e);
+        plan->grp_e[grp] = int32_t(tid);
         plan->grp_res[grp] = 1;
         plan->grp_start[grp] = int32_t(first);
-        for (uint32_t j = 0; j < ntile_e; ++j) {
-            tiles[2 * (tstart + j)] = grp;
-            tiles[2 * (tstart + j) + 1] = first + kExpertTile * j;
-        }
     }
-    if (e < E) hist[uint64_t(n_tiles) * E + e] = first;
-    if (e == 0) {
+    if (tid < E) hist[uint64_t(n_tiles) * E + tid] = first;
+    if (tid == 0) {
         plan->n_groups = total_groups;
         plan->n_entries = N;
         plan->n_miss = 0;
@@ -303,6 +342,17 @@ __global__ __launch_bounds__(512) void group_plan_kernel(uint32_t* __restrict__ 
         plan->n_tiles = total_tiles;
         plan->bad = N - total_count;
         plan->grp_start[total_groups] = int32_t(total_count);
+    }
+    // Every group has at least one tile, so the groups' first tiles ascend strictly.
+    for (uint32_t i = tid; i < total_tiles; i += kScanThreads) {
+        uint32_t lo = 0, hi = total_groups;
+        while (hi - lo > 1u) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (s_tstart[mid] <= i) lo = mid;
+            else hi = mid;
+        }
+        tiles[2 * i] = lo;
+        tiles[2 * i + 1] = s_first[lo] + kExpertTile * (i - s_tstart[lo]);
     }
 }
 
@@ -345,6 +395,105 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(const int32_t* __res
     dst[slot] = int32_t(entry);
 }
 
+// ---------------------------------------------------------------------------------------
+// Expert-stage validation (prefill_moe.metal:603-733): status is cleared, then bit 1 set
+// when the plan header, the tile chain, or the destination permutation is inconsistent.
+// ---------------------------------------------------------------------------------------
+// The header and per-group checks run one group per thread; the tile-count sum is a block
+// reduction, so the whole plan is checked in a few dependent memory round trips.
+// The whole check runs in one workgroup of NT threads; `reset_status` clears the status
+// words first (a full layer's gather leaves that to the grouping, see GroupPrep).
+template <uint32_t NT>
+__device__ __forceinline__ void check_plan(const PlanCheck& c, bool reset_status) {
+    __shared__ uint32_t s_header_ok, s_groups_ok, s_wave_tiles[NT / 64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    if (tid < c.n_counters) c.counters[tid] = 0u;
+    // Address snapshots: every load of a thread is issued before its stores, so the reads
+    // of pinned host memory cost one round trip (tables are at most 3 x 512 words).
+    constexpr int kPer = 1536 / NT;
+    uint64_t v1[kPer], v2[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + NT * j;
+        v1[j] = c.snap_src != nullptr && i < c.snap_words ? c.snap_src[i] : 0u;
+        v2[j] = c.snap_src2 != nullptr && i < c.snap_words2 ? c.snap_src2[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = tid + NT * j;
+        if (c.snap_src != nullptr && i < c.snap_words) c.snap_dst[i] = v1[j];
+        if (c.snap_src2 != nullptr && i < c.snap_words2) c.snap_dst2[i] = v2[j];
+    }
+    const Plan* p = c.plan;
+    const uint32_t N = c.n_entries, E = c.n_experts;
+    const uint32_t ng = p->n_groups, nt = p->n_tiles;
+    auto fail = [&]() {
+        atomicOr(c.status, 2u);
+        if (c.status2 != nullptr) atomicOr(c.status2, 2u);
+    };
+    if (tid == 0) {
+        if (reset_status) {
+            *c.status = 0u;
+            if (c.status2 != nullptr) *c.status2 = 0u;
+        }
+        s_groups_ok = 1u;
+        s_header_ok = (p->bad == 0u && ng != 0u && ng <= E && ng <= 512u && p->n_entries == N &&
+                       nt <= c.tile_capacity && nt <= p->n_entries && p->grp_start[0] == 0 &&
+                       p->grp_start[ng] == int32_t(N))
+                          ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_header_ok) {
+        if (tid == 0) fail();
+        return;
+    }
+    // Group g: non-empty, inside [0, N), expert in range and strictly ascending.
+    uint32_t my_tiles = 0;
+    for (uint32_t g = tid; g < ng; g += NT) {
+        const int32_t first = p->grp_start[g], end = p->grp_start[g + 1], ex = p->grp_e[g];
+        bool ok = end > first && uint32_t(end) <= N && ex >= 0 && uint32_t(ex) < E;
+        if (g != 0u) ok = ok && ex > p->grp_e[g - 1];
+        if (!ok) s_groups_ok = 0u;
+        else my_tiles += (uint32_t(end - first) + kExpertTile - 1) / kExpertTile;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) my_tiles += __shfl_xor(my_tiles, off);
+    if (lane == 0) s_wave_tiles[wave] = my_tiles;
+    __syncthreads();
+    uint32_t expected = 0;
+    for (uint32_t w = 0; w < NT / 64; ++w) expected += s_wave_tiles[w];
+    if (!s_groups_ok || expected != nt) {
+        if (tid == 0) fail();
+        return;
+    }
+    const uint32_t* tiles = c.tiles;
+    for (uint32_t i = tid; i < nt; i += NT) {
+        const uint32_t tg = tiles[2 * i], ty = tiles[2 * i + 1];
+        bool ok = tg < ng;
+        if (ok) {
+            const uint32_t first = uint32_t(p->grp_start[tg]), end = uint32_t(p->grp_start[tg + 1]);
+            ok = ty >= first && ty < end && (ty - first) % kExpertTile == 0u;
+            if (i == 0u) {
+                ok = ok && tg == 0u && ty == 0u;
+            } else {
+                const uint32_t pg = tiles[2 * (i - 1)], py = tiles[2 * (i - 1) + 1];
+                if (pg >= ng) ok = false;
+                else if (pg == tg) ok = ok && ty == py + kExpertTile;
+                else if (pg + 1u == tg) ok = ok && py + kExpertTile >= uint32_t(p->grp_start[pg + 1]) && ty == first;
+                else ok = false;
+            }
+            if (i + 1u == nt) ok = ok && tg + 1u == ng && ty + kExpertTile >= end;
+        }
+        if (!ok) fail();
+    }
+}
+
+__global__ __launch_bounds__(512) void plan_validate_kernel(PlanCheck c) {
+    for (uint32_t i = blockIdx.x * 512u + threadIdx.x; i < c.clear_words; i += gridDim.x * 512u) c.clear[i] = 0u;
+    if (blockIdx.x != 0) return;
+    check_plan<512>(c, true);
+}
+
 // Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. Workgroup b copies the rows of
 // grouped chunk b / 8 (kGatherChunk rows) whose source token lies in token slice b % 8
 // (tokens [T*s/8, T*(s+1)/8)). Every (chunk, slice) pair belongs to one workgroup, so each
@@ -355,17 +504,45 @@ __global__ __launch_bounds__(256) void group_scatter_kernel(const int32_t* __res
 // issuing its loads for those rows before its stores. The stores are non-temporal: the
 // grouped rows are a write-once stream. The plan header is checked first as in the
 // reference's gather (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
+// CHECK (a full layer, both expert stages on the grouping's plan): workgroup 0 runs the
+// stages' plan check (prefill_moe.metal:603-733) and the copy workgroups are 1.. (copy
+// workgroup g = b - 1 takes slice g % 8, so each XCD still reads a single slice). Copy
+// workgroup g also marks destination entries [8g, 8g + 8) in the bitset, which is the
+// reference's destination check (prefill_moe_down_dispatch.mm:470-520) spread over the
+// gather: an entry outside [0, N) or one already marked sets bit 1 of the down status.
 constexpr uint32_t kGatherChunk = 64, kGatherRows = 4;
+template <bool CHECK>
 __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t rows,
                                                      uint32_t vpr, const int32_t* __restrict__ src,
                                                      const Plan* __restrict__ plan, uint32_t N,
-                                                     u32x4* __restrict__ xs) {
+                                                     u32x4* __restrict__ xs, PlanCheck c,
+                                                     const int32_t* __restrict__ dst, uint32_t* __restrict__ bits) {
     static_assert(kGatherChunk == 64, "one wave compacts a chunk");
     __shared__ uint32_t s_row[kGatherChunk], s_tok[kGatherChunk], s_n;
-    const uint32_t tid = threadIdx.x, slice = blockIdx.x & 7u, a = (blockIdx.x >> 3) * kGatherChunk + tid;
+    uint32_t b = blockIdx.x;
+    if constexpr (CHECK) {
+        if (b == 0) {
+            check_plan<256>(c, false);
+            return;
+        }
+        b -= 1u;
+    }
+    const uint32_t tid = threadIdx.x, slice = b & 7u, a = (b >> 3) * kGatherChunk + tid;
     const uint32_t t_lo = uint32_t((uint64_t(rows) * slice) >> 3);
     const uint32_t t_hi = uint32_t((uint64_t(rows) * (slice + 1u)) >> 3);
     const int32_t sv = tid < kGatherChunk && a < N ? src[a] : -1;  // issued before the plan reads
+    if constexpr (CHECK) {
+        const uint32_t i = b * 8u + (tid - 192u);  // wave 3; wave 0 compacts
+        if (tid >= 192u && tid < 200u && i < N) {
+            const uint32_t dv = uint32_t(dst[i]);
+            if (dv >= N) {
+                atomicOr(c.status2, 2u);
+            } else {
+                const uint32_t mask = 1u << (dv % 32u);
+                if (atomicOr(&bits[dv / 32u], mask) & mask) atomicOr(c.status2, 2u);
+            }
+        }
+    }
     const uint32_t ng = plan->n_groups;
     if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) return;
     const int32_t sorted_signed = plan->grp_start[ng];
@@ -393,96 +570,6 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
             for (uint32_t r = 0; r < kGatherRows; ++r)
                 if (i + r < n) __builtin_nontemporal_store(v[r], &xs[uint64_t(s_row[i + r]) * vpr + c]);
         }
-}
-
-// ---------------------------------------------------------------------------------------
-// Expert-stage validation (prefill_moe.metal:603-733): status is cleared, then bit 1 set
-// when the plan header, the tile chain, or the destination permutation is inconsistent.
-// ---------------------------------------------------------------------------------------
-// The header and per-group checks run one group per thread; the tile-count sum is a block
-// reduction, so the whole plan is checked in a few dependent memory round trips.
-__global__ __launch_bounds__(512) void plan_validate_kernel(PlanCheck c) {
-    __shared__ uint32_t s_header_ok, s_groups_ok, s_wave_tiles[8];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    for (uint32_t i = blockIdx.x * 512u + tid; i < c.clear_words; i += gridDim.x * 512u) c.clear[i] = 0u;
-    if (blockIdx.x != 0) return;
-    if (tid < c.n_counters) c.counters[tid] = 0u;
-    // Address snapshots: every load of a thread is issued before its stores, so the reads
-    // of pinned host memory cost one round trip (tables are at most 3 x 512 words).
-    constexpr int kPer = 3;
-    uint64_t v1[kPer], v2[kPer];
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const uint32_t i = tid + 512u * j;
-        v1[j] = c.snap_src != nullptr && i < c.snap_words ? c.snap_src[i] : 0u;
-        v2[j] = c.snap_src2 != nullptr && i < c.snap_words2 ? c.snap_src2[i] : 0u;
-    }
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const uint32_t i = tid + 512u * j;
-        if (c.snap_src != nullptr && i < c.snap_words) c.snap_dst[i] = v1[j];
-        if (c.snap_src2 != nullptr && i < c.snap_words2) c.snap_dst2[i] = v2[j];
-    }
-    const Plan* p = c.plan;
-    const uint32_t N = c.n_entries, E = c.n_experts;
-    const uint32_t ng = p->n_groups, nt = p->n_tiles;
-    auto fail = [&]() {
-        atomicOr(c.status, 2u);
-        if (c.status2 != nullptr) atomicOr(c.status2, 2u);
-    };
-    if (tid == 0) {
-        *c.status = 0u;
-        if (c.status2 != nullptr) *c.status2 = 0u;
-        s_groups_ok = 1u;
-        s_header_ok = (p->bad == 0u && ng != 0u && ng <= E && ng <= 512u && p->n_entries == N &&
-                       nt <= c.tile_capacity && nt <= p->n_entries && p->grp_start[0] == 0 &&
-                       p->grp_start[ng] == int32_t(N))
-                          ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_header_ok) {
-        if (tid == 0) fail();
-        return;
-    }
-    // Group g: non-empty, inside [0, N), expert in range and strictly ascending.
-    uint32_t my_tiles = 0;
-    for (uint32_t g = tid; g < ng; g += 512u) {
-        const int32_t first = p->grp_start[g], end = p->grp_start[g + 1], ex = p->grp_e[g];
-        bool ok = end > first && uint32_t(end) <= N && ex >= 0 && uint32_t(ex) < E;
-        if (g != 0u) ok = ok && ex > p->grp_e[g - 1];
-        if (!ok) s_groups_ok = 0u;
-        else my_tiles += (uint32_t(end - first) + kExpertTile - 1) / kExpertTile;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) my_tiles += __shfl_xor(my_tiles, off);
-    if (lane == 0) s_wave_tiles[wave] = my_tiles;
-    __syncthreads();
-    uint32_t expected = 0;
-    for (uint32_t w = 0; w < 8; ++w) expected += s_wave_tiles[w];
-    if (!s_groups_ok || expected != nt) {
-        if (tid == 0) fail();
-        return;
-    }
-    const uint32_t* tiles = c.tiles;
-    for (uint32_t i = tid; i < nt; i += 512u) {
-        const uint32_t tg = tiles[2 * i], ty = tiles[2 * i + 1];
-        bool ok = tg < ng;
-        if (ok) {
-            const uint32_t first = uint32_t(p->grp_start[tg]), end = uint32_t(p->grp_start[tg + 1]);
-            ok = ty >= first && ty < end && (ty - first) % kExpertTile == 0u;
-            if (i == 0u) {
-                ok = ok && tg == 0u && ty == 0u;
-            } else {
-                const uint32_t pg = tiles[2 * (i - 1)], py = tiles[2 * (i - 1) + 1];
-                if (pg >= ng) ok = false;
-                else if (pg == tg) ok = ok && ty == py + kExpertTile;
-                else if (pg + 1u == tg) ok = ok && py + kExpertTile >= uint32_t(p->grp_start[pg + 1]) && ty == first;
-                else ok = false;
-            }
-            if (i + 1u == nt) ok = ok && tg + 1u == ng && ty + kExpertTile >= end;
-        }
-        if (!ok) fail();
-    }
 }
 
 __global__ __launch_bounds__(256) void bitset_clear_kernel(uint32_t* __restrict__ bits, uint32_t words) {
@@ -534,12 +621,14 @@ hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, 
 }
 
 hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32_t E, uint32_t* hist,
-                           Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst, hipStream_t s) {
+                           Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst, const GroupPrep* prep,
+                           hipStream_t s) {
     const uint32_t N = rows * K;
     const uint32_t n_tiles = (N + kCountTile - 1) / kCountTile;
-    group_count_kernel<<<n_tiles, 256, 0, s>>>(ids, N, E, hist);
-    group_colscan_kernel<<<(E + 31) / 32, 1024, 0, s>>>(hist, E, n_tiles);
-    group_plan_kernel<<<1, 512, 0, s>>>(hist, E, N, n_tiles, plan, tiles);
+    uint32_t* arrive = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(plan) + kArriveBytes);
+    group_count_kernel<<<n_tiles, 256, 0, s>>>(ids, N, E, hist, arrive);
+    group_scan_plan_kernel<<<(E + 31) / 32, kScanThreads, 0, s>>>(hist, E, N, n_tiles, plan, tiles, arrive,
+                                                                  prep != nullptr ? *prep : GroupPrep{});
     group_scatter_kernel<<<n_tiles, 256, 0, s>>>(ids, N, K, E, n_tiles, hist, src, dst);
     return hipGetLastError();
 }
@@ -548,8 +637,19 @@ hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int
                          const Plan* plan, uint32_t N, _Float16* xs, hipStream_t s) {
     const uint32_t vpr = d / 8;
     const uint32_t blocks = 8u * ((N + kGatherChunk - 1) / kGatherChunk);  // (chunk, token slice) pairs
-    gather_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
-                                         reinterpret_cast<u32x4*>(xs));
+    gather_kernel<false><<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
+                                                reinterpret_cast<u32x4*>(xs), PlanCheck{}, nullptr, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_checked(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
+                                 const Plan* plan, uint32_t N, _Float16* xs, const PlanCheck& c,
+                                 const int32_t* dst, uint32_t* bits, hipStream_t s) {
+    if (c.snap_words > 1536u || c.snap_words2 > 1536u || c.status2 == nullptr) return hipErrorInvalidValue;
+    const uint32_t vpr = d / 8;
+    const uint32_t blocks = 1u + 8u * ((N + kGatherChunk - 1) / kGatherChunk);  // check + copy workgroups
+    gather_kernel<true><<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
+                                               reinterpret_cast<u32x4*>(xs), c, dst, bits);
     return hipGetLastError();
 }
 

@@ -254,19 +254,47 @@ bool check_grouping(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& 
            c.view(b.gathered_rows, gath_b, 16, "gathered rows", true, r.gathered);
 }
 
-void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupRes& r) {
+// A full layer whose expert stages share one plan and tile list folds their checks into the
+// grouping and the gather: the grouping's scan workgroup zeroes both status words and the
+// destination bitset, and the gather launch runs the plan check (with the address-table
+// snapshots from the two ring slots) and the destination marks.
+struct LayerChecks {
+    sm::GroupPrep prep;
+    sm::PlanCheck check;
+    const int32_t* dst;
+    uint32_t* bits;
+    int slot1, slot2;
+};
+
+void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupRes& r,
+                            const LayerChecks* lc = nullptr) {
     const auto rows = s.rows, E = s.n_experts, K = s.top_k, d = s.hidden;
+    const bool fused = lc != nullptr;
+    const sm::GroupPrep prep = fused ? lc->prep : sm::GroupPrep{};
     add_step(seg, "grouping", [=](hipStream_t st) {
         return sm::launch_grouping(reinterpret_cast<const int32_t*>(r.ids), rows, K, E,
                                    reinterpret_cast<uint32_t*>(r.hist), reinterpret_cast<sm::Plan*>(r.plan),
                                    reinterpret_cast<uint32_t*>(r.tiles), reinterpret_cast<int32_t*>(r.src),
-                                   reinterpret_cast<int32_t*>(r.dst), st);
+                                   reinterpret_cast<int32_t*>(r.dst), fused ? &prep : nullptr, st);
     });
-    add_step(seg, "gather", [=](hipStream_t st) {
-        return sm::launch_gather(reinterpret_cast<const _Float16*>(r.mixed), rows, d,
-                                 reinterpret_cast<const int32_t*>(r.src), reinterpret_cast<const sm::Plan*>(r.plan),
-                                 rows * K, reinterpret_cast<_Float16*>(r.gathered), st);
+    if (!fused) {
+        add_step(seg, "gather", [=](hipStream_t st) {
+            return sm::launch_gather(reinterpret_cast<const _Float16*>(r.mixed), rows, d,
+                                     reinterpret_cast<const int32_t*>(r.src),
+                                     reinterpret_cast<const sm::Plan*>(r.plan), rows * K,
+                                     reinterpret_cast<_Float16*>(r.gathered), st);
+        });
+        return;
+    }
+    const LayerChecks l = *lc;
+    add_step(seg, "gather + expert checks", [=](hipStream_t st) {
+        return sm::launch_gather_checked(reinterpret_cast<const _Float16*>(r.mixed), rows, d,
+                                         reinterpret_cast<const int32_t*>(r.src),
+                                         reinterpret_cast<const sm::Plan*>(r.plan), rows * K,
+                                         reinterpret_cast<_Float16*>(r.gathered), l.check, l.dst, l.bits, st);
     });
+    seg->steps.back().ring_slot = l.slot1;
+    seg->steps.back().ring_slot2 = l.slot2;
 }
 
 struct RouterRes { uintptr_t x, w, bias, logits; };
@@ -468,41 +496,58 @@ sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, co
     return SM_OK;
 }
 
-// Full layer, both expert stages on one plan and tile list: the plan is checked once, for
-// both status words, and the same launch copies both address snapshots and clears the
-// destination bitset. Stages with distinct plan or tile views are encoded separately.
+// Both expert stages on one plan and tile list: the plan is checked once, for both status
+// words, and the same launch copies both address snapshots and clears the destination
+// bitset. Claims the two ring slots (released again if the second claim fails).
+struct ExpertsPlan {
+    sm::RoutedGemm g, d;
+    sm::PlanCheck check;
+    int slot1, slot2;
+};
+sm_status prepare_experts(sm_segment* seg, const sm_moe_shape& s, int fmt_gu, const GateUpRes& gu, int fmt_dn,
+                          const DownRes& dn, ExpertsPlan& x) {
+    x.slot1 = claim_ring_slot(seg->ctx, gu.w.table);
+    if (claim_status(x.slot1) != SM_OK) return claim_status(x.slot1);
+    x.slot2 = claim_ring_slot(seg->ctx, dn.w.table);
+    if (claim_status(x.slot2) != SM_OK) {
+        if (x.slot1 >= 0) {
+            std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
+            seg->ctx->ring_claimed[x.slot1] = false;
+        }
+        return claim_status(x.slot2);
+    }
+    x.g = gate_up_gemm(s, fmt_gu, gu);
+    x.d = down_gemm(s, fmt_dn, dn);
+    sm::PlanCheck& c = x.check;
+    c = stage_check(seg->ctx, x.g, x.slot1, gu.w.snapshot, uint32_t(gu.w.table.size()));
+    const sm::PlanCheck c2 = stage_check(seg->ctx, x.d, x.slot2, dn.w.snapshot, uint32_t(dn.w.table.size()));
+    c.status2 = x.d.status;
+    c.snap_src2 = c2.snap_src;
+    c.snap_dst2 = c2.snap_dst;
+    c.snap_words2 = c2.snap_words;
+    c.clear = reinterpret_cast<uint32_t*>(x.d.out_f);
+    c.clear_words = uint32_t(ceil_div(x.d.n_entries, 32));
+    c.n_counters = 2 * sm::kCounterWords;  // gate/up's counters, then down's
+    return SM_OK;
+}
+
+// Stages with distinct plan or tile views are encoded separately.
 sm_status encode_experts_launch(sm_segment* seg, const sm_moe_shape& s, int fmt_gu, const GateUpRes& gu, int fmt_dn,
                                 const DownRes& dn) {
     if (gu.plan != dn.plan || gu.tiles != dn.tiles) {
         sm_status st = encode_gate_up_launch(seg, s, fmt_gu, gu);
         return st != SM_OK ? st : encode_down_launch(seg, s, fmt_dn, dn);
     }
-    const int slot1 = claim_ring_slot(seg->ctx, gu.w.table);
-    if (claim_status(slot1) != SM_OK) return claim_status(slot1);
-    const int slot2 = claim_ring_slot(seg->ctx, dn.w.table);
-    if (claim_status(slot2) != SM_OK) {
-        if (slot1 >= 0) {
-            std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
-            seg->ctx->ring_claimed[slot1] = false;
-        }
-        return claim_status(slot2);
-    }
-    const sm::RoutedGemm g = gate_up_gemm(s, fmt_gu, gu);
-    const sm::RoutedGemm d = down_gemm(s, fmt_dn, dn);
-    sm::PlanCheck c = stage_check(seg->ctx, g, slot1, gu.w.snapshot, uint32_t(gu.w.table.size()));
-    const sm::PlanCheck c2 = stage_check(seg->ctx, d, slot2, dn.w.snapshot, uint32_t(dn.w.table.size()));
-    c.status2 = d.status;
-    c.snap_src2 = c2.snap_src;
-    c.snap_dst2 = c2.snap_dst;
-    c.snap_words2 = c2.snap_words;
-    c.clear = reinterpret_cast<uint32_t*>(d.out_f);
-    c.clear_words = uint32_t(ceil_div(d.n_entries, 32));
-    c.n_counters = 2 * sm::kCounterWords;  // gate/up's counters, then down's
+    ExpertsPlan x;
+    const sm_status st = prepare_experts(seg, s, fmt_gu, gu, fmt_dn, dn, x);
+    if (st != SM_OK) return st;
+    const sm::PlanCheck c = x.check;
+    const sm::RoutedGemm g = x.g;
     add_step(seg, "expert plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
-    seg->steps.back().ring_slot = slot1;
-    seg->steps.back().ring_slot2 = slot2;
+    seg->steps.back().ring_slot = x.slot1;
+    seg->steps.back().ring_slot2 = x.slot2;
     add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fmt_gu), g, st); });
-    add_down_tail(seg, fmt_dn, d, false);
+    add_down_tail(seg, fmt_dn, x.d, false);
     return SM_OK;
 }
 
@@ -872,7 +917,7 @@ bool check_route_gather(Check& c, const sm_moe_shape& s, const sm_route_gather_b
 }
 
 void encode_route_gather_launch(sm_segment* seg, const sm_moe_shape& s, const RouterRes& rr, const RouteRes& ro,
-                                const GroupRes& gr) {
+                                const GroupRes& gr, const LayerChecks* lc = nullptr) {
     const auto rows = s.rows, d = s.hidden, E = s.n_experts;
     add_step(seg, "router GEMM", [=](hipStream_t st) {
         return sm::launch_router_gemm(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
@@ -880,7 +925,7 @@ void encode_route_gather_launch(sm_segment* seg, const sm_moe_shape& s, const Ro
                                       rows, d, E, st);
     });
     encode_route_launch(seg, s, 1, ro);
-    encode_grouping_launch(seg, s, gr);
+    encode_grouping_launch(seg, s, gr, lc);
 }
 }  // namespace
 
@@ -1056,10 +1101,35 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
     // The shared expert waits for the work recorded before this layer (in a segment of
     // several layers, the previous layer), not for this layer's routing.
     const size_t first = seg->steps.size();
-    encode_route_gather_launch(seg, s, rr, ro, gr);
-    seg->steps[first].fork_before = true;
-    if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
-    if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
+    if (gu.plan == dn.plan && gu.tiles == dn.tiles) {
+        // One plan for both expert stages: their checks ride on the grouping and the gather.
+        ExpertsPlan x;
+        if ((st = prepare_experts(seg, s, f->gate_up, gu, f->down, dn, x)) != SM_OK) return ring_fail(seg, st);
+        LayerChecks lc{};
+        lc.prep.status = x.g.status;
+        lc.prep.status2 = x.d.status;
+        lc.prep.clear = x.check.clear;
+        lc.prep.clear_words = x.check.clear_words;
+        lc.check = x.check;
+        lc.check.clear = nullptr;
+        lc.check.clear_words = 0;
+        lc.dst = x.d.dst;
+        lc.bits = x.check.clear;
+        lc.slot1 = x.slot1;
+        lc.slot2 = x.slot2;
+        encode_route_gather_launch(seg, s, rr, ro, gr, &lc);
+        seg->steps[first].fork_before = true;
+        if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
+        const sm::RoutedGemm g = x.g, d = x.d;
+        const int fg = f->gate_up, fd = f->down;
+        add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fg), g, st); });
+        add_step(seg, "down tiles", [=](hipStream_t st) { return sm::launch_down(Fmt(fd), d, st); });
+    } else {
+        encode_route_gather_launch(seg, s, rr, ro, gr);
+        seg->steps[first].fork_before = true;
+        if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
+        if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
+    }
     encode_combine_launch(seg, s, co, has_shared);
     return SM_OK;
 }

@@ -107,7 +107,8 @@ def fake(moe):
 def test_valid_layer_encodes(fake):
     ok, err, n = fake.encode()
     assert ok, err
-    assert n >= 12  # router, top-k, 4 grouping, gather, shared x3, validators, tiles, combine
+    # router, top-k, grouping, gather with the expert checks, shared x3, gate/up, down, combine
+    assert n == 10
 
 
 def test_commit_without_device_reports_device_error(moe, fake):

@@ -136,3 +136,74 @@ def test_full_layer_clears_both_status_words_and_reports_null_address(moe, layer
     seg.commit(stream)
     bad, st_gu, st_dn = ws.read_status(stream)
     assert (bad, st_gu, st_dn) == (0, 1, 0)
+
+
+def _foreign(gpu_ctx, tensor, dtype, edit):
+    host = gu.host(tensor, dtype).copy()
+    edit(host)
+    return gpu_ctx.register(gu.dev(host))
+
+
+@pytest.mark.parametrize("fault", ["repeat", "out_of_range"])
+def test_full_layer_checks_destinations_in_the_gather(moe, layer, orc, gpu_ctx, stream, fault):
+    """A full layer whose down stage reads a destination map other than the grouping's: the
+    gather launch marks it in the bitset, a repeated or out-of-range entry sets bit 1 of the
+    down status only, and the down tiles write zeros (metal_prefill_moe_full_pipeline_test.mm:
+    1081-1104 permutation faults)."""
+    print(f"case failure full layer destination {fault}", flush=True)
+    cfg, inp, ws = _small_layer(moe, layer, gpu_ctx)
+    ws.run_layer(stream)
+    N = cfg.rows * cfg.top_k
+
+    def edit(d):
+        if fault == "repeat":
+            d[5] = d[6]
+        else:
+            d[N - 1] = N
+
+    bad_dst = _foreign(gpu_ctx, ws.dst, np.int32, edit)
+    lb = ws.layer_buffers()
+    lb.down = moe.DownBuffers(ws.dn_table.struct, ws.hidden.view(), ws.plan.view(), ws.tiles.view(),
+                              bad_dst.view(), ws.parts.view(), ws.status.view(4, 4))
+    ws.status.tensor.fill_(-1)
+    ws.parts.tensor.fill_(7.0)
+    seg = gpu_ctx.segment()
+    ok, err = seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, lb, keep=(ws, bad_dst))
+    assert ok, err
+    seg.commit(stream)
+    bad, st_gu, st_dn = ws.read_status(stream)
+    assert (bad, st_gu, st_dn) == (0, 0, 2)
+    assert (gu.host(ws.parts, np.float32) == 0).all()
+    # The same layer on the grouping's own map is clean again (the bitset is cleared per call).
+    ws.run_layer(stream)
+    assert ws.read_status(stream) == (0, 0, 0)
+
+
+def test_full_layer_checks_a_foreign_plan_in_the_gather(moe, layer, orc, gpu_ctx, stream):
+    """Both expert stages bound to one plan and tile list other than the grouping's, with a
+    broken tile chain: the plan check in the gather launch sets bit 1 of both status words and
+    both stages write zeros (prefill_moe.metal:603-733)."""
+    print("case failure full layer foreign plan", flush=True)
+    cfg, inp, ws = _small_layer(moe, layer, gpu_ctx)
+    ws.run_layer(stream)
+    plan2 = _foreign(gpu_ctx, ws.plan, np.uint8, lambda p: None)
+
+    def edit(t):
+        t[3] += 1                                    # second tile's first entry off the 64 grid
+    tiles2 = _foreign(gpu_ctx, ws.tiles, np.uint32, edit)
+    lb = ws.layer_buffers()
+    lb.gate_up = moe.GateUpBuffers(ws.gu_table.struct, ws.xs.view(), plan2.view(), tiles2.view(),
+                                   ws.hidden.view(), ws.status.view(0, 4))
+    lb.down = moe.DownBuffers(ws.dn_table.struct, ws.hidden.view(), plan2.view(), tiles2.view(),
+                              ws.dst.view(), ws.parts.view(), ws.status.view(4, 4))
+    ws.status.tensor.fill_(-1)
+    ws.hidden.tensor.fill_(0x7C01)
+    ws.parts.tensor.fill_(7.0)
+    seg = gpu_ctx.segment()
+    ok, err = seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, lb, keep=(ws, plan2, tiles2))
+    assert ok, err
+    seg.commit(stream)
+    bad, st_gu, st_dn = ws.read_status(stream)
+    assert (bad, st_gu, st_dn) == (0, 2, 2)
+    assert (gu.host(ws.hidden, np.uint16) == 0).all()
+    assert (gu.host(ws.parts, np.float32) == 0).all()
