@@ -16,16 +16,37 @@ constexpr float kWeightFloor = 6.103515625e-5f;  // 2^-14
 // products and are merged as fma(lo, 2^-11, hi). Tile: ROWS tokens (32, 64 or 128) x 64
 // experts per 256-thread workgroup; wave w owns experts 16w..16w+15. Each expert's weights
 // are read and split once per workgroup, so larger token tiles divide that work; the
-// launcher takes the largest tile that still gives every CU a workgroup. The ROWS x 256
-// activation slab is copied by LDS-DMA into a double-buffered, XOR-swizzled LDS ring; each
-// lane's 64 F32 weights of the next slab are in flight in registers while the current slab
-// is split and multiplied.
+// launcher takes the largest tile that still gives every CU a workgroup.
+// The reduction is streamed in stages of 64 columns through an LDS ring of NST slots: each
+// stage holds the ROWS x 64 activation slab and the 64 x 64 F32 weight slab, both copied by
+// LDS-DMA (16 bytes per lane, XOR-swizzled chunk positions), and the copies run NST - 1
+// stages ahead, so a wave waits only for the oldest stage while the later ones stay in
+// flight (one workgroup per CU has no other work to hide the memory latency behind). The
+// ring stays within 96 KB so that a workgroup of the shared expert's GEMM, which runs beside
+// the router on the second stream, still fits on the same CU. K-steps keep the order of a
+// plain loop over k, so the sums are those of a one-stage pipeline.
 // ---------------------------------------------------------------------------------------
 constexpr int kRouterCols = 64;
-constexpr int kSlab = 256;
 
-// Position (16-byte chunks) of chunk c of row r in a swizzled rows x 256 slab.
-__device__ __forceinline__ uint32_t slab_pos(uint32_t r, uint32_t c) { return r * 32u + (c ^ (r & 15u)); }
+template <int ROWS>
+struct RouterStage {
+    static constexpr int KS = 64;                      // reduction columns per stage
+    static constexpr int NST = ROWS == 128 ? 3 : 4;    // ring slots (NST - 1 stages in flight)
+    static constexpr int CPR = KS / 8;                 // 16-byte activation chunks per row
+    static constexpr int RPI = 64 / CPR;               // activation rows per copy instruction
+    static constexpr int NA = ROWS / (4 * RPI);        // activation copies per wave and stage
+    static constexpr int WCPR = KS / 4;                // 16-byte weight chunks per expert row
+    static constexpr int WPI = 64 / WCPR;              // expert rows per copy instruction
+    static constexpr int NW = 16 / WPI;                // weight copies per wave (its 16 experts)
+    static constexpr int A_BYTES = ROWS * KS * 2;
+    static constexpr int BYTES = A_BYTES + kRouterCols * KS * 4;
+    static_assert(NA * 4 * RPI == ROWS && NW * WPI == 16, "copy map covers the stage");
+    static_assert(NST * BYTES <= 96 * 1024, "LDS ring leaves room for a co-resident workgroup");
+};
+
+// s_waitcnt immediate that waits for at most n vector-memory operations (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their no-wait maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 template <int ROWS>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __restrict__ x,
@@ -33,87 +54,123 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
                                                           const float* __restrict__ bias,
                                                           float* __restrict__ logits,
                                                           uint32_t rows, uint32_t d, uint32_t E) {
-    constexpr int RB = ROWS / 16;    // 16-row MFMA blocks
-    constexpr int NJ = ROWS / 8;     // activation copy instructions per wave and slab
-    __shared__ __attribute__((aligned(1024))) _Float16 sa[2][ROWS * kSlab];
+    using S = RouterStage<ROWS>;
+    constexpr int RB = ROWS / 16;  // 16-row MFMA blocks
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[S::NST * S::BYTES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const uint32_t t0 = blockIdx.x * ROWS;
     const uint32_t e0 = blockIdx.y * kRouterCols;
     const uint32_t e = e0 + 16 * wave + n;
     const bool e_ok = e < E;
-    // K mapping: k-step s feeds lane group g the values 32s + 8g .. 32s + 8g + 7 of a slab,
-    // so the four lane groups of an expert row read one contiguous 128-byte piece per
-    // k-step (row 0 stands in for experts past E; those outputs are never stored).
-    const float* wrow = w + uint64_t(e_ok ? e : 0) * d + 8 * g;
-    // Activation copy map: wave instruction q = NJ*wave + j fills chunk positions
-    // [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk (lane & 31) ^ (R & 15). Row
-    // offsets are kept in halves (rows x d < 2^32 is checked by the launcher).
-    uint32_t aofs[NJ];
+    // Copy maps (element offsets at k = 0; rows x d < 2^32 is checked by the launcher).
+    // Activation copy q = NA*wave + j fills LDS chunk positions [64q, 64q + 64): row
+    // R = RPI*q + lane / CPR, position p = lane % CPR holding chunk p ^ (R % CPR).
+    uint32_t aofs[S::NA];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const uint32_t R = 2u * (uint32_t(NJ) * wave + j) + (uint32_t(lane) >> 5);
-        const uint32_t C = (uint32_t(lane) & 31u) ^ (R & 15u);
+    for (int j = 0; j < S::NA; ++j) {
+        const uint32_t R = uint32_t(S::RPI * (S::NA * wave + j)) + uint32_t(lane) / S::CPR;
+        const uint32_t C = (uint32_t(lane) % S::CPR) ^ (R % S::CPR);
         const uint32_t t = t0 + R < rows ? t0 + R : rows - 1u;
         aofs[j] = t * d + 8u * C;
     }
-    auto issue_a = [&](uint32_t k0, _Float16* slab) {
+    // Weight copy q = NW*wave + j: expert row Rw = WPI*q + lane / WCPR of the tile (wave w
+    // copies its own 16 experts), position p = lane % WCPR holding chunk p ^ (Rw & 15).
+    // Row 0 stands in for experts past E; those outputs are never stored.
+    uint32_t wofs[S::NW];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
+    for (int j = 0; j < S::NW; ++j) {
+        const uint32_t Rw = uint32_t(S::WPI * (S::NW * wave + j)) + uint32_t(lane) / S::WCPR;
+        const uint32_t C = (uint32_t(lane) % S::WCPR) ^ (Rw & 15u);
+        wofs[j] = (e0 + Rw < E ? e0 + Rw : 0u) * d + 4u * C;
+    }
+    auto issue = [&](uint32_t st, uint32_t slot) {
+        uint8_t* base = ring + slot * S::BYTES;
+        const uint32_t k0 = st * S::KS;
+#pragma unroll
+        for (int j = 0; j < S::NA; ++j)
             __builtin_amdgcn_global_load_lds(
                 reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(x + aofs[j] + k0)),
                 reinterpret_cast<__attribute__((address_space(3))) void*>(
-                    reinterpret_cast<uintptr_t>(slab + (NJ * wave + j) * 512)),
+                    reinterpret_cast<uintptr_t>(base + (S::NA * wave + j) * 1024)),
                 16, 0, 0);
-    };
-    float4v cw[16], nw[16];
-    auto load_w = [&](uint32_t k0, float4v (&dst)[16]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dst[i] = ld_global<float4v>(wrow + k0 + 32 * (i >> 1) + 4 * (i & 1));
+        for (int j = 0; j < S::NW; ++j)
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(w + wofs[j] + k0)),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(base + S::A_BYTES + (S::NW * wave + j) * 1024)),
+                16, 0, 0);
     };
     float4v acc_hi[RB], acc_lo[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
-    const uint32_t n_slabs = d / kSlab;
-    issue_a(0, sa[0]);
-    load_w(0, cw);
-    for (uint32_t sb = 0; sb < n_slabs; ++sb) {
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this slab's activations and weights
-        __syncthreads();                                       // ... from every wave
-        if (sb + 1 < n_slabs) {
-            issue_a((sb + 1) * kSlab, sa[(sb + 1) & 1u]);
-            load_w((sb + 1) * kSlab, nw);
-        }
-        const _Float16* buf = sa[sb & 1u];
+    const uint32_t n_st = d / S::KS;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+    for (int i = 0; i < S::NST - 1; ++i)
+        if (uint32_t(i) < n_st) issue(i, i);
+    const uint32_t wrow = 16u * wave + n;  // this lane's expert row in the weight slab
+    for (uint32_t st = 0; st < n_st; ++st) {
+        // Stage st's copies (of every wave, hence the barrier); stage st + 1 may stay in flight.
+        // A bare s_barrier: __syncthreads() would add a workgroup release that waits for every
+        // copy in flight. This wave's stage-st copies are complete after the wait, and the
+        // slot refilled below was last read in the previous iteration, whose LDS reads every
+        // wave consumed before reaching this barrier.
+        const uint32_t later = n_st - 1u - st;  // stages issued after st (at most NST - 2)
+        if (S::NST == 4 && later >= 2u) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (S::NA + S::NW)));
+        else if (later >= 1u) __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::NA + S::NW));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();
+        if (st + S::NST - 1 < n_st) issue(st + S::NST - 1, (st + S::NST - 1) % S::NST);
+        const uint8_t* base = ring + (st % S::NST) * S::BYTES;
+        const uint8_t* wb = base + S::A_BYTES + wrow * (S::KS * 4);
+#pragma unroll
+        for (int s = 0; s < S::KS / 32; ++s) {
+            // k-step s: lane group g holds columns 32s + 8g .. 32s + 8g + 7 of the stage.
+            const uint32_t c0 = 8u * s + 2u * g;
+            const float4v w0 = *reinterpret_cast<const float4v*>(wb + 16u * (c0 ^ uint32_t(n)));
+            const float4v w1 = *reinterpret_cast<const float4v*>(wb + 16u * ((c0 + 1u) ^ uint32_t(n)));
             half8 bh, bl;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float wf = cw[2 * s + i / 4][i % 4];
+                const float wf = i < 4 ? w0[i] : w1[i - 4];
                 const _Float16 h = _Float16(wf);
                 bh[i] = h;
                 bl[i] = _Float16((wf - float(h)) * 2048.0f);
             }
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                const half8 a = *reinterpret_cast<const half8*>(buf + 8u * slab_pos(16u * rb + n, 4u * s + g));
+                const uint32_t r = 16u * rb + n;
+                const uint32_t pos = (4u * s + g) ^ (r % S::CPR);
+                const half8 a = *reinterpret_cast<const half8*>(base + r * (S::KS * 2) + 16u * pos);
                 acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_hi[rb], 0, 0, 0);
                 acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_lo[rb], 0, 0, 0);
             }
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) cw[i] = nw[i];
     }
     if (!e_ok) return;
     const float b = bias != nullptr ? bias[e] : 0.0f;
+    float v[RB][4];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t t = t0 + 16 * rb + 4 * g + i;
-            if (t < rows) logits[uint64_t(t) * E + e] = __builtin_fmaf(acc_lo[rb][i], 4.8828125e-4f, acc_hi[rb][i]) + b;
-        }
+        for (int i = 0; i < 4; ++i) v[rb][i] = __builtin_fmaf(acc_lo[rb][i], 4.8828125e-4f, acc_hi[rb][i]) + b;
+    // A full token tile stores without per-row branches, so the bias load is waited for once
+    // (a wait per branch would also wait for each earlier store).
+    if (t0 + ROWS <= rows) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) logits[uint64_t(t0 + 16 * rb + 4 * g + i) * E + e] = v[rb][i];
+    } else {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = t0 + 16 * rb + 4 * g + i;
+                if (t < rows) logits[uint64_t(t) * E + e] = v[rb][i];
+            }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
