@@ -175,11 +175,28 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
 
 // ---------------------------------------------------------------------------------------
 // Softmax top-k. One token per half-wave: the 32 lanes of a half replay the reference's
-// 32-lane SIMD group exactly (moe.metal:28-86) — lane L holds experts L + 32i, the max and
-// sum butterflies use xor offsets 16..1, and each round's argmax butterfly prefers the
-// larger value and, on equal values, the lower expert id. Slots past E are padding: they
+// 32-lane SIMD group exactly (moe.metal:28-86) — lane L holds experts L + 32i, the sum
+// butterflies use xor offsets 16..1, and each round's argmax prefers the larger value and,
+// on equal values, the lower expert id. The maximum and the argmax do not depend on the
+// combination order, so they reduce each 16-lane row by DPP and then swap across the two
+// rows; only the sums keep the reference's xor order. Slots past E are padding: they
 // take no part in the sums and hold -inf so they are never selected (top_k <= E).
 // ---------------------------------------------------------------------------------------
+// One step of an order-free reduction within 16-lane rows by DPP (CTRL: quad_perm [1,0,3,2]
+// = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_ror:4 = 0x124, row_ror:8 = 0x128; after all four
+// every lane of a row holds the row's result). Used only where the result does not depend
+// on the combination order: the maximum, and the argmax under "larger value, then lower id".
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& best, int32_t& who) {
+    const float ob = dpp_f<CTRL>(best);
+    const int32_t ow = __builtin_amdgcn_mov_dpp(who, CTRL, 0xF, 0xF, false);
+    if (ob > best || (ob == best && ow < who)) { best = ob; who = ow; }
+}
+
 template <int NV>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
                                                          int32_t* __restrict__ ids,
@@ -198,8 +215,11 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
         v[i] = (live && idx < E) ? row[idx] : kNegInf;
         mx = __builtin_fmaxf(mx, v[i]);
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
+    mx = __builtin_fmaxf(mx, dpp_f<0xB1>(mx));
+    mx = __builtin_fmaxf(mx, dpp_f<0x4E>(mx));
+    mx = __builtin_fmaxf(mx, dpp_f<0x124>(mx));
+    mx = __builtin_fmaxf(mx, dpp_f<0x128>(mx));
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -227,10 +247,13 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 #pragma unroll
         for (int i = 1; i < NV; ++i)
             if (v[i] > best) { best = v[i]; who = int32_t(L + 32u * i); }
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) {
-            const float ob = __shfl_xor(best, off);
-            const int32_t ow = __shfl_xor(who, off);
+        argmax_step<0xB1>(best, who);
+        argmax_step<0x4E>(best, who);
+        argmax_step<0x124>(best, who);
+        argmax_step<0x128>(best, who);
+        {
+            const float ob = __shfl_xor(best, 16);
+            const int32_t ow = __shfl_xor(who, 16);
             if (ob > best || (ob == best && ow < who)) { best = ob; who = ow; }
         }
         if ((uint32_t(who) & 31u) == L) {
