@@ -1047,6 +1047,13 @@ sm_status sm_encode_dequant(sm_segment* seg, sm_format fmt, uint32_t n_out, uint
     return SM_OK;
 }
 
+// Where a full layer's shared expert forks off: beside the router GEMM (offset 0) or, for
+// layers of at least 8192 tokens, after top-k (offset 2: the router and top-k run first).
+// Measured on MI355X: at 2048 tokens the shared GEMMs fit in the router's and the
+// grouping's idle CUs (forking after top-k was 8 us slower), at 8192 tokens they slow the
+// larger router GEMM down (forking after top-k was 17 us faster).
+static size_t shared_fork_offset(const sm_moe_shape& s) { return s.rows >= 8192 ? 2 : 0; }
+
 sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
                                const sm_layer_buffers* b) {
     const char* P = "full-mode Prefill MoE";
@@ -1118,7 +1125,7 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
         lc.slot1 = x.slot1;
         lc.slot2 = x.slot2;
         encode_route_gather_launch(seg, s, rr, ro, gr, &lc);
-        seg->steps[first].fork_before = true;
+        seg->steps[first + shared_fork_offset(s)].fork_before = true;
         if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
         const sm::RoutedGemm g = x.g, d = x.d;
         const int fg = f->gate_up, fd = f->down;
@@ -1126,7 +1133,7 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
         add_step(seg, "down tiles", [=](hipStream_t st) { return sm::launch_down(Fmt(fd), d, st); });
     } else {
         encode_route_gather_launch(seg, s, rr, ro, gr);
-        seg->steps[first].fork_before = true;
+        seg->steps[first + shared_fork_offset(s)].fork_before = true;
         if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
         if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
     }
