@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SM_ABI_VERSION 1u
+#define SM_ABI_VERSION 2u
 
 /* Error classes; each maps onto a class of reference validation message
  * (prefill_moe_grouping_dispatch.mm:84-254, prefill_moe_full_pipeline.cpp:451-475). */
@@ -165,12 +165,16 @@ typedef struct sm_route_gather_buffers {
     sm_view router_bias;      /* F32 [E] added to the logits; null view = none            */
 } sm_route_gather_buffers;
 
-/* Routed expert weights: a host copy of the [E][3] device-address table (gate, up, down;
- * 0 = missing) as the reference keeps per layer (prefill_moe_expert_dispatch.hpp:21-22),
- * validated against the declared storage views (prefill_moe_expert_dispatch.mm:377-448)
- * and copied at commit into `address_snapshot` (device, E*3*8 bytes) before the kernels. */
+/* Routed expert weights: a host copy of the model's [layer][E][3] device-address table
+ * (gate, up, down; 0 = missing), as the reference keeps it (prefill_moe_expert_dispatch.hpp:
+ * 21-22). `layer` selects row layer*E*3 of the n_layers rows, as the reference's `layer`
+ * argument does (prefill_moe_expert_dispatch.mm:259-266); that row is validated against the
+ * declared storage views (prefill_moe_expert_dispatch.mm:377-448) and copied at commit into
+ * `address_snapshot` (device, E*3*8 bytes) before the kernels. */
 typedef struct sm_expert_weights {
     const uint64_t* addresses;
+    uint32_t n_layers;          /* rows of `addresses` (layer < n_layers)                   */
+    uint32_t layer;
     sm_view address_snapshot;
     const sm_view* storage;
     uint32_t n_storage;
@@ -274,6 +278,45 @@ sm_status sm_encode_dequant(sm_segment* seg, sm_format fmt, uint32_t n_out, uint
 sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b);
 
+/* ---- chunk driver (the reference's Prefill::run chunk loop) ------------------------------ */
+/* PrefillChunkSchedule (include/strata/metal/prefill.hpp:47-72): a prompt of token_count
+ * tokens starting at cell pos0, split into contiguous, unpadded ranges of at most chunk_rows. */
+typedef struct sm_chunk_schedule {
+    uint32_t pos0;
+    uint32_t chunk_rows;
+    uint64_t token_count;
+} sm_chunk_schedule;
+/* PrefillChunkRange (prefill.hpp:40-45). */
+typedef struct sm_chunk_range {
+    uint64_t token_offset;
+    uint32_t pos0;
+    uint32_t rows;
+} sm_chunk_range;
+/* build_prefill_chunk_schedule (prefill.hpp:74-88, src/metal/engine/prefill.cpp:57-83):
+ * chunk_rows must be 1..SM_MAX_ROWS and the prompt's positions must fit a signed 32-bit
+ * StepRow; an empty prompt gives an empty schedule. `out` is unchanged on failure. */
+sm_status sm_build_chunk_schedule(uint32_t pos0, uint64_t token_count, uint32_t chunk_rows,
+                                  sm_chunk_schedule* out, char* err, size_t cap);
+/* PrefillChunkSchedule::chunk_count (prefill.hpp:53-57). */
+uint64_t sm_chunk_count(const sm_chunk_schedule* schedule);
+/* PrefillChunkSchedule::range_at (prefill.cpp:39-55): 1 and the range, or 0 with `out`
+ * unchanged for an index past the last range. */
+int sm_chunk_range_at(const sm_chunk_schedule* schedule, uint64_t index, sm_chunk_range* out);
+
+/* The MoE layer over a whole prompt, one full-mode layer call per range of `schedule`, in
+ * order, in one segment (Prefill::run's per-chunk MoE, 04-metal-kernels.md:3701-3891):
+ * chunk k reads rows [token_offset, token_offset + rows) of `input` (F16 [token_count][d])
+ * and writes the same rows of `output` (F32 [token_count][d]). Every other view of `b` is
+ * chunk scratch sized for shape->rows == schedule->chunk_rows rows and reused by every chunk;
+ * stream order serialises the chunks. b->route_gather.mixed_h, b->shared.mixed_h and
+ * b->combine.output are not used (the chunk slices of `input` and `output` replace them).
+ * The two status words are cleared before the first chunk only, so after completion they
+ * hold the OR over every chunk (a route id outside [0, E) in any chunk shows as bit 1); the
+ * plan slot's `bad` field is the last chunk's. */
+sm_status sm_encode_prefill_moe_chunks(sm_segment* seg, const sm_chunk_schedule* schedule,
+                                       const sm_moe_shape* shape, const sm_layer_formats* formats,
+                                       sm_view input, sm_view output, const sm_layer_buffers* b);
+
 /* ---- coordinators: standalone transactional form ---------------------------------------- */
 sm_status sm_submit_route(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                           int divide_weights, const sm_route_buffers* b, char* err, size_t cap);
@@ -296,6 +339,10 @@ sm_status sm_submit_dequant(sm_context* ctx, void* stream, sm_format fmt, uint32
 sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b,
                                char* err, size_t cap);
+sm_status sm_submit_prefill_moe_chunks(sm_context* ctx, void* stream, const sm_chunk_schedule* schedule,
+                                       const sm_moe_shape* shape, const sm_layer_formats* formats,
+                                       sm_view input, sm_view output, const sm_layer_buffers* b, char* err,
+                                       size_t cap);
 
 /* ---- after completion ----------------------------------------------------------------- */
 /* Synchronises `stream`, then reads the plan's `bad` count and up to two status words

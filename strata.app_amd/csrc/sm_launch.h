@@ -80,6 +80,8 @@ struct PlanCheck {
     uint32_t clear_words;
     uint32_t* counters;         // tile-kernel work counters to zero (may be null)
     uint32_t n_counters;
+    uint32_t keep_status;       // non-zero: the status words are not cleared first (they
+                                // accumulate over the chunks of one prompt)
 };
 hipError_t launch_plan_validate(const PlanCheck& c, hipStream_t s);
 // The gather of a full layer with both expert stages' checks in the same launch: one extra

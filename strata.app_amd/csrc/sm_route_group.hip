@@ -63,26 +63,26 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
     const uint32_t e0 = blockIdx.y * kRouterCols;
     const uint32_t e = e0 + 16 * wave + n;
     const bool e_ok = e < E;
-    // Copy maps (element offsets at k = 0; rows x d < 2^32 is checked by the launcher).
+    // Copy maps (element offsets at k = 0, in 64 bits: rows x d may exceed 2^32).
     // Activation copy q = NA*wave + j fills LDS chunk positions [64q, 64q + 64): row
     // R = RPI*q + lane / CPR, position p = lane % CPR holding chunk p ^ (R % CPR).
-    uint32_t aofs[S::NA];
+    uint64_t aofs[S::NA];
 #pragma unroll
     for (int j = 0; j < S::NA; ++j) {
         const uint32_t R = uint32_t(S::RPI * (S::NA * wave + j)) + uint32_t(lane) / S::CPR;
         const uint32_t C = (uint32_t(lane) % S::CPR) ^ (R % S::CPR);
         const uint32_t t = t0 + R < rows ? t0 + R : rows - 1u;
-        aofs[j] = t * d + 8u * C;
+        aofs[j] = uint64_t(t) * d + 8u * C;
     }
     // Weight copy q = NW*wave + j: expert row Rw = WPI*q + lane / WCPR of the tile (wave w
     // copies its own 16 experts), position p = lane % WCPR holding chunk p ^ (Rw & 15).
     // Row 0 stands in for experts past E; those outputs are never stored.
-    uint32_t wofs[S::NW];
+    uint64_t wofs[S::NW];
 #pragma unroll
     for (int j = 0; j < S::NW; ++j) {
         const uint32_t Rw = uint32_t(S::WPI * (S::NW * wave + j)) + uint32_t(lane) / S::WCPR;
         const uint32_t C = (uint32_t(lane) % S::WCPR) ^ (Rw & 15u);
-        wofs[j] = (e0 + Rw < E ? e0 + Rw : 0u) * d + 4u * C;
+        wofs[j] = uint64_t(e0 + Rw < E ? e0 + Rw : 0u) * d + 4u * C;
     }
     auto issue = [&](uint32_t st, uint32_t slot) {
         uint8_t* base = ring + slot * S::BYTES;
@@ -329,9 +329,9 @@ __device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* wave_tot, u
 // Column scan, then the plan. Workgroup c scans expert columns [32c, 32c + 32): thread
 // (slice, e) takes a contiguous run of tiles, the slice partials give each run's exclusive
 // start, each run is rewritten in place with its column prefix, and the column total goes to
-// the extra row hist[n_tiles][e] (a device-coherent store, waited for). Each workgroup then
-// counts itself in at `arrive` (zeroed by the count kernel, which runs just before), and the
-// last to arrive reads the totals with device-coherent loads and builds the plan: block
+// the extra row hist[n_tiles][e] (a device-coherent store). Each workgroup then counts itself
+// in at `arrive` (zeroed by the count kernel, which runs just before) with an acquire-release
+// add, and the last to arrive reads the totals with device-coherent loads and builds the plan: block
 // scans over the experts give each expert's first slot, group index and first tile; the slot
 // is filled, the group fields written, tile i finds its group by binary search over the
 // groups' first tiles (no serial per-expert loop), and hist[n_tiles][e] becomes the expert's
@@ -367,8 +367,8 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
         if (e < E) {
             uint32_t run = 0;
             for (uint32_t sl = 0; sl < slice; ++sl) run += part[sl][el];
-            // The total is the only value another workgroup reads in this launch: a
-            // device-coherent store (no L2-wide write-back needed).
+            // The total is the only value another workgroup reads in this launch: an
+            // agent-scope atomic store, published by the acquire-release add on `arrive`.
             if (slice == 31u)
                 __hip_atomic_store(&hist[uint64_t(n_tiles) * E + e], run + local, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -380,11 +380,15 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
             }
         }
     }
-    // Count in once this workgroup's totals are stored; the last to arrive reads all totals
-    // with device-coherent loads. The rewritten rows are read only by the scatter launch.
-    __builtin_amdgcn_s_waitcnt(0);
+    // Count in once this workgroup's totals are stored: the workgroup barrier orders every
+    // thread's total before thread 0's acquire-release add on `arrive` (agent scope), and the
+    // last workgroup to arrive acquires every earlier workgroup's totals through that same
+    // word before its barrier hands them to its other threads. The rewritten rows are read
+    // only by the scatter launch.
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(arrive, 1u) == gridDim.x - 1u ? 1u : 0u;
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1u
+                     ? 1u : 0u;
     __syncthreads();
     if (!s_last) return;
 
@@ -571,7 +575,7 @@ __device__ __forceinline__ void check_plan(const PlanCheck& c, bool reset_status
 __global__ __launch_bounds__(512) void plan_validate_kernel(PlanCheck c) {
     for (uint32_t i = blockIdx.x * 512u + threadIdx.x; i < c.clear_words; i += gridDim.x * 512u) c.clear[i] = 0u;
     if (blockIdx.x != 0) return;
-    check_plan<512>(c, true);
+    check_plan<512>(c, c.keep_status == 0u);
 }
 
 // Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. Workgroup b copies the rows of
@@ -676,11 +680,10 @@ hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bi
     // The largest token tile that still launches at least one workgroup per CU (256), so
     // each expert's weights are split as few times as the layer allows.
     const uint32_t ecols = (E + kRouterCols - 1) / kRouterCols;
-    const bool fits = uint64_t(rows) * d < (1ull << 32);
     auto blocks = [&](uint32_t r) { return ((rows + r - 1) / r) * ecols; };
-    if (fits && blocks(128) >= 256u) {
+    if (blocks(128) >= 256u) {
         router_gemm_kernel<128><<<dim3((rows + 127) / 128, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
-    } else if (fits && blocks(64) >= 256u) {
+    } else if (blocks(64) >= 256u) {
         router_gemm_kernel<64><<<dim3((rows + 63) / 64, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
     } else {
         router_gemm_kernel<32><<<dim3((rows + 31) / 32, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);

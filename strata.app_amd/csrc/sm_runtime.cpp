@@ -162,6 +162,16 @@ struct Check {
         return true;
     }
 
+    // An expert stage's plan view: the PfPlan fields are read, and the stage's work-item
+    // counters in the slot's padding (`words` u32 at byte `counter_off`) are written, so the
+    // view is registered as a read-only PfPlan range and a writable counter range.
+    bool plan_view(const sm_view& v, uint32_t counter_off, uint32_t words, uintptr_t& out) {
+        if (!view(v, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", false, out)) return false;
+        inputs.back().bytes = sm::kCounterBytes;
+        outputs.push_back({out + counter_off, 4ull * words, "work counters", true, stage});
+        return true;
+    }
+
     // Outputs must be disjoint from every input and from each other
     // (prefill_moe_grouping_dispatch.mm:234-252).
     bool aliases() {
@@ -305,6 +315,8 @@ struct WeightsRes { uintptr_t snapshot; std::vector<uint64_t> table; };
 bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, int fmt, bool gate_up,
                    WeightsRes& r) {
     if (w.addresses == nullptr) return c.fail(SM_E_ARGUMENT, c.prefix + " address table is null");
+    if (w.layer >= w.n_layers)
+        return c.fail(SM_E_ARGUMENT, c.prefix + " layer is outside the address table");
     const uint64_t E = s.n_experts;
     if (!c.view(w.address_snapshot, E * 3 * 8, 8, "address snapshot", true, r.snapshot)) return false;
     const uint64_t per_row = gate_up ? fmt_row_bytes(fmt, s.hidden) : fmt_row_bytes(fmt, s.expert_ff);
@@ -318,7 +330,8 @@ bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, 
         if (!c.view(v, v.length, 1, "weight storage", false, p)) return false;
         storage.push_back({p, v.length, "weight storage", false, c.stage});
     }
-    r.table.assign(w.addresses, w.addresses + E * 3);
+    const uint64_t* row = w.addresses + uint64_t(w.layer) * E * 3;  // the selected layer's [E][3]
+    r.table.assign(row, row + E * 3);
     const uint64_t align = weight_align(fmt);
     for (uint64_t e = 0; e < E; ++e) {
         for (int role = 0; role < 3; ++role) {
@@ -379,7 +392,7 @@ bool check_gate_up(Check& c, const sm_moe_shape& s, int fmt, const sm_gate_up_bu
         return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
     return check_weights(c, s, b.weights, fmt, true, r.w) &&
            c.view(b.gathered_rows, xs_b, 16, "gathered rows", false, r.xs) &&
-           c.view(b.plan, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", false, r.plan) &&
+           c.plan_view(b.plan, sm::kCounterBytes, sm::kCounterWords, r.plan) &&
            c.view(b.tiles, tiles_b, 8, "tile list", false, r.tiles) &&
            c.view(b.hidden, h_b, 16, "hidden", true, r.hidden) &&
            c.view(b.status, 4, 4, "status", true, r.status);
@@ -424,11 +437,30 @@ sm::PlanCheck stage_check(sm_context* ctx, const sm::RoutedGemm& g, int slot, ui
 
 sm_status claim_status(int slot) { return slot == -2 ? SM_E_SEGMENT : slot == -3 ? SM_E_DEVICE : SM_OK; }
 
-sm_status encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r) {
-    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+// The chunks of one prompt (sm_encode_prefill_moe_chunks) run the same layer over the same
+// weights: the first chunk claims the pinned ring slots of the address tables and the later
+// chunks read the same slots, and only the first chunk clears the status words.
+struct ChunkCtl {
+    bool keep_status = false;
+    int slot_gu = -9, slot_dn = -9;  // -9: not claimed yet
+};
+
+// A ring slot for one expert stage: the chunk's slot when it has one, else a new claim
+// (recorded in the chunk control for the later chunks).
+int stage_slot(sm_segment* seg, const std::vector<uint64_t>& table, int* chunk_slot) {
+    if (chunk_slot != nullptr && *chunk_slot != -9) return *chunk_slot;
+    const int slot = claim_ring_slot(seg->ctx, table);
+    if (chunk_slot != nullptr && claim_status(slot) == SM_OK) *chunk_slot = slot;
+    return slot;
+}
+
+sm_status encode_gate_up_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const GateUpRes& r,
+                                ChunkCtl* ctl = nullptr) {
+    const int slot = stage_slot(seg, r.w.table, ctl ? &ctl->slot_gu : nullptr);
     if (claim_status(slot) != SM_OK) return claim_status(slot);
     const sm::RoutedGemm g = gate_up_gemm(s, fmt, r);
-    const sm::PlanCheck c = stage_check(seg->ctx, g, slot, r.w.snapshot, uint32_t(r.w.table.size()));
+    sm::PlanCheck c = stage_check(seg->ctx, g, slot, r.w.snapshot, uint32_t(r.w.table.size()));
+    c.keep_status = ctl && ctl->keep_status ? 1u : 0u;
     add_step(seg, "gate/up plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
     seg->steps.back().ring_slot = slot;
     add_step(seg, "gate/up tiles", [=](hipStream_t st) { return sm::launch_gate_up(Fmt(fmt), g, st); });
@@ -447,7 +479,7 @@ bool check_down(Check& c, const sm_moe_shape& s, int fmt, const sm_down_buffers&
         return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
     return check_weights(c, s, b.weights, fmt, false, r.w) &&
            c.view(b.hidden, h_b, 16, "hidden", false, r.hidden) &&
-           c.view(b.plan, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", false, r.plan) &&
+           c.plan_view(b.plan, sm::kCounterBytes + 4 * sm::kCounterWords, sm::kCounterWords, r.plan) &&
            c.view(b.tiles, tiles_b, 8, "tile list", false, r.tiles) &&
            c.view(b.destinations, N * 4, 4, "destinations", false, r.dst) &&
            c.view(b.parts, p_b, 16, "parts", true, r.parts) &&
@@ -485,11 +517,13 @@ void add_down_tail(sm_segment* seg, int fmt, const sm::RoutedGemm& g, bool bitse
     add_step(seg, "down tiles", [=](hipStream_t st) { return sm::launch_down(Fmt(fmt), g, st); });
 }
 
-sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r) {
-    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+sm_status encode_down_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const DownRes& r,
+                             ChunkCtl* ctl = nullptr) {
+    const int slot = stage_slot(seg, r.w.table, ctl ? &ctl->slot_dn : nullptr);
     if (claim_status(slot) != SM_OK) return claim_status(slot);
     const sm::RoutedGemm g = down_gemm(s, fmt, r);
-    const sm::PlanCheck c = stage_check(seg->ctx, g, slot, r.w.snapshot, uint32_t(r.w.table.size()));
+    sm::PlanCheck c = stage_check(seg->ctx, g, slot, r.w.snapshot, uint32_t(r.w.table.size()));
+    c.keep_status = ctl && ctl->keep_status ? 1u : 0u;
     add_step(seg, "down plan validate", [=](hipStream_t st) { return sm::launch_plan_validate(c, st); });
     seg->steps.back().ring_slot = slot;
     add_down_tail(seg, fmt, g, true);
@@ -505,12 +539,13 @@ struct ExpertsPlan {
     int slot1, slot2;
 };
 sm_status prepare_experts(sm_segment* seg, const sm_moe_shape& s, int fmt_gu, const GateUpRes& gu, int fmt_dn,
-                          const DownRes& dn, ExpertsPlan& x) {
-    x.slot1 = claim_ring_slot(seg->ctx, gu.w.table);
+                          const DownRes& dn, ExpertsPlan& x, ChunkCtl* ctl = nullptr) {
+    const bool had_gu = ctl != nullptr && ctl->slot_gu != -9;
+    x.slot1 = stage_slot(seg, gu.w.table, ctl ? &ctl->slot_gu : nullptr);
     if (claim_status(x.slot1) != SM_OK) return claim_status(x.slot1);
-    x.slot2 = claim_ring_slot(seg->ctx, dn.w.table);
+    x.slot2 = stage_slot(seg, dn.w.table, ctl ? &ctl->slot_dn : nullptr);
     if (claim_status(x.slot2) != SM_OK) {
-        if (x.slot1 >= 0) {
+        if (x.slot1 >= 0 && !had_gu) {
             std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
             seg->ctx->ring_claimed[x.slot1] = false;
         }
@@ -528,18 +563,19 @@ sm_status prepare_experts(sm_segment* seg, const sm_moe_shape& s, int fmt_gu, co
     c.clear = reinterpret_cast<uint32_t*>(x.d.out_f);
     c.clear_words = uint32_t(ceil_div(x.d.n_entries, 32));
     c.n_counters = 2 * sm::kCounterWords;  // gate/up's counters, then down's
+    c.keep_status = ctl && ctl->keep_status ? 1u : 0u;
     return SM_OK;
 }
 
 // Stages with distinct plan or tile views are encoded separately.
 sm_status encode_experts_launch(sm_segment* seg, const sm_moe_shape& s, int fmt_gu, const GateUpRes& gu, int fmt_dn,
-                                const DownRes& dn) {
+                                const DownRes& dn, ChunkCtl* ctl = nullptr) {
     if (gu.plan != dn.plan || gu.tiles != dn.tiles) {
-        sm_status st = encode_gate_up_launch(seg, s, fmt_gu, gu);
-        return st != SM_OK ? st : encode_down_launch(seg, s, fmt_dn, dn);
+        sm_status st = encode_gate_up_launch(seg, s, fmt_gu, gu, ctl);
+        return st != SM_OK ? st : encode_down_launch(seg, s, fmt_dn, dn, ctl);
     }
     ExpertsPlan x;
-    const sm_status st = prepare_experts(seg, s, fmt_gu, gu, fmt_dn, dn, x);
+    const sm_status st = prepare_experts(seg, s, fmt_gu, gu, fmt_dn, dn, x, ctl);
     if (st != SM_OK) return st;
     const sm::PlanCheck c = x.check;
     const sm::RoutedGemm g = x.g;
@@ -658,7 +694,17 @@ bool expected_edge(const Range& w, const Range& r) {
         {"shared.gate logit", "combine.gate"},           {"gate_up.hidden", "down.hidden"},
         {"down.parts", "combine.parts"},
     };
-    if (!w.writable || r.writable || w.stage >= r.stage) return false;
+    if (!w.writable || w.stage >= r.stage) return false;
+    // The expert stages' work counters lie in the padding of the plan slot the grouping
+    // wrote; each stage owns its own words, so a later stage may write inside that range.
+    static const char* const scratch[][2] = {
+        {"route.PfPlan slot", "gate_up.work counters"}, {"route.PfPlan slot", "down.work counters"},
+    };
+    if (r.writable) {
+        for (const auto& e : scratch)
+            if (w.name == e[0] && r.name == e[1]) return r.ptr >= w.ptr && r.ptr + r.bytes <= w.ptr + w.bytes;
+        return false;
+    }
     for (const auto& e : edges)
         if (w.name == e[0] && r.name == e[1]) return w.ptr == r.ptr && r.bytes <= w.bytes;
     return false;
@@ -777,16 +823,22 @@ sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
         if (st == SM_OK && hipEventRecord(ctx->fork_ev, stream) != hipSuccess) st = SM_E_DEVICE;
         fork_pending = true;
     };
+    // Also after a failed launch: the caller's stream must not run ahead of side launches
+    // already queued (a caller may free the buffers they write once its stream is idle).
+    // If the join itself cannot be recorded, the side stream is drained instead.
     auto join = [&]() {
-        if (st == SM_OK && (hipEventRecord(ctx->join_ev, ctx->side) != hipSuccess ||
-                            hipStreamWaitEvent(stream, ctx->join_ev, 0) != hipSuccess))
+        if (hipEventRecord(ctx->join_ev, ctx->side) != hipSuccess ||
+            hipStreamWaitEvent(stream, ctx->join_ev, 0) != hipSuccess) {
+            (void)hipStreamSynchronize(ctx->side);  // best effort; the failure is reported below
             st = SM_E_DEVICE;
+        }
         side_open = false;
     };
     for (size_t i = 0; i < seg->steps.size(); ++i) {
         auto& step = seg->steps[i];
         if (st != SM_OK) break;
         if (step.join && side_open) join();
+        if (st != SM_OK) break;
         if (use_side && step.fork_before) fork();
         const hipStream_t hs = use_side && step.side ? ctx->side : stream;
         if (hs != stream) {
@@ -1054,8 +1106,9 @@ sm_status sm_encode_dequant(sm_segment* seg, sm_format fmt, uint32_t n_out, uint
 // larger router GEMM down (forking after top-k was 17 us faster).
 static size_t shared_fork_offset(const sm_moe_shape& s) { return s.rows >= 8192 ? 2 : 0; }
 
-sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
-                               const sm_layer_buffers* b) {
+namespace {
+sm_status encode_full_layer_impl(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
+                                 const sm_layer_buffers* b, ChunkCtl* ctl) {
     const char* P = "full-mode Prefill MoE";
     if (seg == nullptr) return SM_E_ARGUMENT;
     if (seg->failed) return SM_E_SEGMENT;
@@ -1098,8 +1151,10 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
             const Range& a = all[i];
             const Range& bb = all[j];
             if (a.stage == bb.stage || !overlap(a, bb) || (!a.writable && !bb.writable)) continue;
-            const Range& w = a.writable ? a : bb;
-            const Range& r = a.writable ? bb : a;
+            // Writer first: the earlier stage when both write.
+            const bool a_first = a.writable && (!bb.writable || a.stage < bb.stage);
+            const Range& w = a_first ? a : bb;
+            const Range& r = a_first ? bb : a;
             if (expected_edge(w, r)) continue;
             return record_fail(seg, SM_E_ALIAS, std::string(P) + " " + w.name + " overlaps active " + r.name);
         }
@@ -1111,10 +1166,12 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
     if (gu.plan == dn.plan && gu.tiles == dn.tiles) {
         // One plan for both expert stages: their checks ride on the grouping and the gather.
         ExpertsPlan x;
-        if ((st = prepare_experts(seg, s, f->gate_up, gu, f->down, dn, x)) != SM_OK) return ring_fail(seg, st);
+        if ((st = prepare_experts(seg, s, f->gate_up, gu, f->down, dn, x, ctl)) != SM_OK) return ring_fail(seg, st);
         LayerChecks lc{};
-        lc.prep.status = x.g.status;
-        lc.prep.status2 = x.d.status;
+        if (!(ctl && ctl->keep_status)) {
+            lc.prep.status = x.g.status;
+            lc.prep.status2 = x.d.status;
+        }
         lc.prep.clear = x.check.clear;
         lc.prep.clear_words = x.check.clear_words;
         lc.check = x.check;
@@ -1135,9 +1192,90 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const
         encode_route_gather_launch(seg, s, rr, ro, gr);
         seg->steps[first + shared_fork_offset(s)].fork_before = true;
         if (has_shared) encode_shared_launch(seg, s, f->shared, sr, true);
-        if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn)) != SM_OK) return ring_fail(seg, st);
+        if ((st = encode_experts_launch(seg, s, f->gate_up, gu, f->down, dn, ctl)) != SM_OK) return ring_fail(seg, st);
     }
     encode_combine_launch(seg, s, co, has_shared);
+    return SM_OK;
+}
+}  // namespace
+
+sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
+                               const sm_layer_buffers* b) {
+    return encode_full_layer_impl(seg, shape, f, b, nullptr);
+}
+
+// ---- chunk driver ---------------------------------------------------------------------
+
+sm_status sm_build_chunk_schedule(uint32_t pos0, uint64_t token_count, uint32_t chunk_rows, sm_chunk_schedule* out,
+                                  char* err, size_t cap) {
+    auto fail = [&](const char* msg) {
+        if (err && cap) std::snprintf(err, cap, "%s", msg);
+        return SM_E_SHAPE;
+    };
+    if (out == nullptr) return SM_E_ARGUMENT;
+    if (chunk_rows == 0 || chunk_rows > SM_MAX_ROWS) return fail("Prefill chunk size must fit the shader row limit");
+    // Every position p0 + t must fit a signed 32-bit StepRow (n_kv = pos + 1 included).
+    const uint64_t max_step = uint64_t(std::numeric_limits<int32_t>::max());
+    if (token_count != 0 && (pos0 >= max_step || token_count > max_step - pos0))
+        return fail("Prefill prompt positions exceed the signed StepRow range");
+    *out = sm_chunk_schedule{pos0, chunk_rows, token_count};
+    if (err && cap) err[0] = 0;
+    return SM_OK;
+}
+
+uint64_t sm_chunk_count(const sm_chunk_schedule* s) {
+    if (s == nullptr || s->token_count == 0 || s->chunk_rows == 0) return 0;
+    return 1 + (s->token_count - 1) / s->chunk_rows;
+}
+
+int sm_chunk_range_at(const sm_chunk_schedule* s, uint64_t index, sm_chunk_range* out) {
+    if (s == nullptr || out == nullptr || index >= sm_chunk_count(s)) return 0;
+    const uint64_t off = index * s->chunk_rows;
+    const uint64_t rows = std::min<uint64_t>(s->token_count - off, s->chunk_rows);
+    *out = sm_chunk_range{off, uint32_t(uint64_t(s->pos0) + off), uint32_t(rows)};
+    return 1;
+}
+
+sm_status sm_encode_prefill_moe_chunks(sm_segment* seg, const sm_chunk_schedule* schedule, const sm_moe_shape* shape,
+                                       const sm_layer_formats* f, sm_view input, sm_view output,
+                                       const sm_layer_buffers* b) {
+    const char* P = "Prefill MoE chunks";
+    if (seg == nullptr) return SM_E_ARGUMENT;
+    if (seg->failed) return SM_E_SEGMENT;
+    if (!schedule || !shape || !f || !b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " arguments are null");
+    if (schedule->chunk_rows == 0 || schedule->chunk_rows > SM_MAX_ROWS)
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " chunk size must fit the shader row limit");
+    if (shape->rows != schedule->chunk_rows)
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " scratch rows must equal the schedule's chunk size");
+    const uint64_t n = sm_chunk_count(schedule);
+    if (n == 0) return SM_OK;
+    // The whole prompt's input and output views: owned, large enough, output apart from input.
+    Check c;
+    c.ctx = seg->ctx;
+    c.prefix = P;
+    uint64_t in_b, out_b;
+    if (!mul_ok({schedule->token_count, shape->hidden, 2}, in_b) || !mul_ok({schedule->token_count, shape->hidden, 4}, out_b))
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " buffer size overflows");
+    uintptr_t pin, pout;
+    if (!c.view(input, in_b, 16, "input rows", false, pin) || !c.view(output, out_b, 16, "output rows", true, pout) ||
+        !c.aliases())
+        return finish(seg, c);
+    ChunkCtl ctl;
+    for (uint64_t k = 0; k < n; ++k) {
+        sm_chunk_range r{};
+        sm_chunk_range_at(schedule, k, &r);
+        sm_moe_shape cs = *shape;
+        cs.rows = r.rows;
+        sm_layer_buffers lb = *b;
+        const sm_view xin{input.buffer, input.offset + r.token_offset * shape->hidden * 2, uint64_t(r.rows) * shape->hidden * 2};
+        lb.route_gather.mixed_h = xin;
+        lb.shared.mixed_h = xin;
+        lb.combine.output = sm_view{output.buffer, output.offset + r.token_offset * shape->hidden * 4,
+                                    uint64_t(r.rows) * shape->hidden * 4};
+        ctl.keep_status = k > 0;
+        const sm_status st = encode_full_layer_impl(seg, &cs, f, &lb, &ctl);
+        if (st != SM_OK) return st;  // the segment is poisoned with the chunk's message
+    }
     return SM_OK;
 }
 
@@ -1198,6 +1336,12 @@ sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape
                                const sm_layer_formats* formats, const sm_layer_buffers* b, char* err,
                                size_t cap) {
     SM_SUBMIT_BODY(sm_encode_full_layer(seg, shape, formats, b))
+}
+
+sm_status sm_submit_prefill_moe_chunks(sm_context* ctx, void* stream, const sm_chunk_schedule* schedule,
+                                       const sm_moe_shape* shape, const sm_layer_formats* formats, sm_view input,
+                                       sm_view output, const sm_layer_buffers* b, char* err, size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_prefill_moe_chunks(seg, schedule, shape, formats, input, output, b))
 }
 
 sm_status sm_read_layer_status(sm_context* ctx, void* stream, sm_view plan, sm_view gu, sm_view dn,

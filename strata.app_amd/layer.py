@@ -226,6 +226,42 @@ class LayerWorkspace:
                                           self.status.view(4, 4))
 
 
+class PromptWorkspace:
+    """The chunk driver over a whole prompt: the prompt's input rows (F16 [chunks*T, d]) and output
+    rows (F32), and one chunk's scratch (a LayerWorkspace of `cfg.rows` rows) that every chunk
+    reuses. One segment runs every chunk (sm_encode_prefill_moe_chunks)."""
+
+    def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0"):
+        import torch
+        self.ctx, self.cfg = ctx, cfg
+        self.chunk = LayerWorkspace(ctx, cfg, inputs, device, chunk=0)
+        n = cfg.rows * cfg.chunks
+        dev = torch.device(device)
+        self.x_all = ctx.register(_dev(inputs.x.view(np.uint16).view(np.int16), dev))
+        self.out_all = ctx.register(torch.empty(n * cfg.hidden, dtype=torch.float32, device=dev))
+        sched, err = moe.build_chunk_schedule(0, n, cfg.rows)
+        if sched is None:
+            raise ValueError(err)
+        self.schedule = sched
+
+    def encode(self, seg: moe.Segment):
+        ws = self.chunk
+        self._lb = ws.layer_buffers()
+        return seg.encode_prefill_moe_chunks(self.schedule, ws.shape, ws.formats, self.x_all.view(),
+                                             self.out_all.view(), self._lb, keep=self)
+
+    def run(self, stream=0) -> None:
+        seg = self.ctx.segment()
+        ok, err = self.encode(seg)
+        if not ok:
+            seg.abort()
+            raise RuntimeError(err)
+        seg.commit(stream)
+
+    def read_status(self, stream=0):
+        return self.chunk.read_status(stream)
+
+
 def layer_flops(cfg: LayerConfig) -> float:
     """Algorithmic FLOPs of one layer call (router, gate/up, down, shared)."""
     T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
@@ -237,5 +273,5 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
-__all__ = ["LayerConfig", "CONFIGS", "HostInputs", "make_inputs", "LayerWorkspace", "layer_flops",
-           "zipf_bias"]
+__all__ = ["LayerConfig", "CONFIGS", "HostInputs", "make_inputs", "LayerWorkspace", "PromptWorkspace",
+           "layer_flops", "zipf_bias"]

@@ -43,6 +43,8 @@ EXPORTS = (
     "sm_submit_route", "sm_submit_grouping", "sm_submit_route_gather", "sm_submit_shared_ffn",
     "sm_submit_gate_up", "sm_submit_down", "sm_submit_swiglu", "sm_submit_combine",
     "sm_submit_full_layer", "sm_read_layer_status",
+    "sm_build_chunk_schedule", "sm_chunk_count", "sm_chunk_range_at", "sm_encode_prefill_moe_chunks",
+    "sm_submit_prefill_moe_chunks",
     "sm_synth_normal_f32", "sm_synth_normal_f16", "sm_synth_normal_bf16", "sm_quantize",
     "sm_synth_quantized",
 )
@@ -78,8 +80,8 @@ class RouteGatherBuffers(C.Structure):
 
 
 class ExpertWeights(C.Structure):
-    _fields_ = [("addresses", C.POINTER(C.c_uint64)), ("address_snapshot", View),
-                ("storage", C.POINTER(View)), ("n_storage", C.c_uint32)]
+    _fields_ = [("addresses", C.POINTER(C.c_uint64)), ("n_layers", C.c_uint32), ("layer", C.c_uint32),
+                ("address_snapshot", View), ("storage", C.POINTER(View)), ("n_storage", C.c_uint32)]
 
 
 class GateUpBuffers(C.Structure):
@@ -115,6 +117,16 @@ class LayerBuffers(C.Structure):
     _fields_ = [("route_gather", RouteGatherBuffers), ("shared", SharedBuffers),
                 ("gate_up", GateUpBuffers), ("down", DownBuffers),
                 ("combine", CombineBuffers)]
+
+
+class ChunkSchedule(C.Structure):
+    """PrefillChunkSchedule (include/strata/metal/prefill.hpp:47-72)."""
+    _fields_ = [("pos0", C.c_uint32), ("chunk_rows", C.c_uint32), ("token_count", C.c_uint64)]
+
+
+class ChunkRange(C.Structure):
+    """PrefillChunkRange (prefill.hpp:40-45)."""
+    _fields_ = [("token_offset", C.c_uint64), ("pos0", C.c_uint32), ("rows", C.c_uint32)]
 
 
 _lib: Optional[C.CDLL] = None
@@ -167,6 +179,14 @@ def library() -> C.CDLL:
                                      C.POINTER(LayerBuffers), C.c_char_p, C.c_size_t]),
         "sm_read_layer_status": (I, [P, P, View, View, View, C.POINTER(U32), C.POINTER(U32),
                                      C.POINTER(U32)]),
+        "sm_build_chunk_schedule": (I, [U32, U64, U32, C.POINTER(ChunkSchedule), C.c_char_p, C.c_size_t]),
+        "sm_chunk_count": (U64, [C.POINTER(ChunkSchedule)]),
+        "sm_chunk_range_at": (I, [C.POINTER(ChunkSchedule), U64, C.POINTER(ChunkRange)]),
+        "sm_encode_prefill_moe_chunks": (I, [P, C.POINTER(ChunkSchedule), C.POINTER(Shape), C.POINTER(LayerFormats),
+                                             View, View, C.POINTER(LayerBuffers)]),
+        "sm_submit_prefill_moe_chunks": (I, [P, P, C.POINTER(ChunkSchedule), C.POINTER(Shape),
+                                             C.POINTER(LayerFormats), View, View, C.POINTER(LayerBuffers),
+                                             C.c_char_p, C.c_size_t]),
         "sm_synth_normal_f32": (None, [U64, U64, C.c_float, P, U64]),
         "sm_synth_normal_f16": (None, [U64, U64, C.c_float, P, U64]),
         "sm_synth_normal_bf16": (None, [U64, U64, C.c_float, P, U64]),
@@ -279,14 +299,35 @@ class Context:
 
 
 class ExpertTable:
-    """Host copy of the [E][3] (gate, up, down) expert address table plus its storage."""
+    """Host copy of the [layer][E][3] (gate, up, down) expert address table plus its storage;
+    `layer` selects the row the stage reads (the reference's `layer` argument)."""
 
-    def __init__(self, addresses: Sequence[int], snapshot: View, storage: Sequence[View]):
+    def __init__(self, addresses: Sequence[int], snapshot: View, storage: Sequence[View], n_layers: int = 1,
+                 layer: int = 0):
         n = len(addresses)
         self._addr = (C.c_uint64 * n)(*addresses)
         self._storage = (View * max(1, len(storage)))(*storage)
-        self.struct = ExpertWeights(C.cast(self._addr, C.POINTER(C.c_uint64)), snapshot,
+        self.struct = ExpertWeights(C.cast(self._addr, C.POINTER(C.c_uint64)), n_layers, layer, snapshot,
                                     C.cast(self._storage, C.POINTER(View)), len(storage))
+
+
+def build_chunk_schedule(pos0: int, token_count: int, chunk_rows: int):
+    """build_prefill_chunk_schedule: (ChunkSchedule, "") or (None, error message)."""
+    out = ChunkSchedule()
+    err = C.create_string_buffer(256)
+    st = library().sm_build_chunk_schedule(pos0, token_count, chunk_rows, C.byref(out), err, 256)
+    return (out, "") if st == 0 else (None, err.value.decode())
+
+
+def chunk_ranges(schedule: ChunkSchedule):
+    """Every PrefillChunkRange of a schedule, in order (range_at over chunk_count)."""
+    lib = library()
+    out = []
+    for i in range(int(lib.sm_chunk_count(C.byref(schedule)))):
+        r = ChunkRange()
+        assert lib.sm_chunk_range_at(C.byref(schedule), i, C.byref(r)) == 1
+        out.append((int(r.token_offset), int(r.pos0), int(r.rows)))
+    return out
 
 
 class Segment:
@@ -347,6 +388,13 @@ class Segment:
         self._keep.append(keep)
         return self._ret(self.lib.sm_encode_full_layer(self.handle, C.byref(shape), C.byref(formats),
                                                        C.byref(b)))
+
+    def encode_prefill_moe_chunks(self, schedule: ChunkSchedule, shape: Shape, formats: LayerFormats, input: View,
+                                  output: View, b: LayerBuffers, keep=None):
+        """The layer over every range of a chunk schedule (Prefill::run's per-chunk MoE)."""
+        self._keep.append((schedule, keep))
+        return self._ret(self.lib.sm_encode_prefill_moe_chunks(self.handle, C.byref(schedule), C.byref(shape),
+                                                               C.byref(formats), input, output, C.byref(b)))
 
     def encode_prefill_dequant(self, fmt: int, n_out: int, k: int, weights: View, k_major_f16: View):
         return self._ret(self.lib.sm_encode_dequant(self.handle, fmt, n_out, k, weights, k_major_f16))

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol(moe):
     missing = [d for d in sorted(declared) if not hasattr(lib, d)]
     assert not missing, missing
     assert set(moe.EXPORTS) <= declared
-    assert lib.sm_abi_version() == 1
+    assert lib.sm_abi_version() == 2
 
 
 def test_scratch_size_helpers(moe):
@@ -258,3 +258,49 @@ def test_stage_coordinators_validate_independently(moe, fake):
                                                                       fake.rw.view()))
     seg.abort()
     assert not ok and "route IDs overlaps active logits" in err
+
+
+def test_expert_stage_plan_counters_are_written(moe, fake):
+    """The expert stages write their work counters in the plan slot's padding, so a plan view
+    whose padding overlaps another view of the stage is rejected (a read-only registration would
+    have let it through and the counters would overwrite the tile list)."""
+    lb = fake.layer()
+    # One allocation holding the plan slot and, from byte 6208 on, the tile list: the PfPlan
+    # fields (bytes 0..6207) stay clear of the tile list, the counter words do not.
+    nt = moe.tiles_bytes(fake.shape)
+    both = fake.buf(6400 + nt)
+    plan_over_tiles = both.view(0, 6400)
+    gu = moe.GateUpBuffers(lb.gate_up.weights, lb.gate_up.gathered_rows, plan_over_tiles, both.view(6208, nt),
+                           lb.gate_up.hidden, lb.gate_up.status)
+    seg = fake.ctx.segment()
+    ok, err = seg.encode_prefill_moe_gu(fake.shape, moe.Q4_K, gu)
+    seg.abort()
+    assert not ok and "work counters overlaps active tile list" in err
+    dn = moe.DownBuffers(lb.down.weights, lb.down.hidden, plan_over_tiles, both.view(6240, nt), lb.down.destinations,
+                         lb.down.parts, lb.down.status)
+    seg = fake.ctx.segment()
+    ok, err = seg.encode_prefill_moe_down(fake.shape, moe.Q8_0, dn)
+    seg.abort()
+    assert not ok and "work counters overlaps active tile list" in err
+    # The full layer accepts the grouping's own plan slot feeding both stages' counters.
+    assert fake.encode()[0]
+
+
+def test_route_gather_accepts_rows_times_hidden_past_2_32(moe):
+    """Activation offsets are 64-bit in every kernel of the route/gather stage, so a chunk whose
+    rows x hidden exceeds 2^32 elements is accepted (262,208 rows x 16,384)."""
+    f = Fake.__new__(Fake)
+    f.moe, f.ctx, f.n = moe, moe.Context(0), 0
+    f.STRIDE = 1 << 36
+    T, d, E, K = 262208, 16384, 16, 1
+    s = moe.Shape(T, d, E, K, 128, 0)
+    b = f.buf
+    x, w, lg, ids, rw = b(T * d * 2), b(E * d * 4), b(T * E * 4), b(T * K * 4), b(T * K * 4)
+    hist, plan, tiles = b(moe.histogram_bytes(s)), b(6400), b(moe.tiles_bytes(s))
+    src, dst, xs = b(T * K * 4), b(T * K * 4), b(T * K * d * 2)
+    rg = moe.RouteGatherBuffers(x.view(), w.view(), lg.view(), ids.view(), rw.view(), hist.view(), plan.view(),
+                                tiles.view(), src.view(), dst.view(), xs.view(), moe.NULL_VIEW)
+    seg = f.ctx.segment()
+    ok, err = seg.encode_prefill_moe_full_mode_route_gather(s, rg)
+    seg.abort()
+    assert ok, err

@@ -107,3 +107,19 @@ def test_combine_and_swiglu_against_reference_twins(orc):
     h = orc.swiglu(g, u).view(np.float16).astype(np.float64)
     tw = twin.astype(np.float16).astype(np.float64)
     assert (np.abs(h - tw) <= np.maximum(np.abs(tw) * 2.0 ** -10, 2.0 ** -24)).all()  # <= 1 half-ULP
+
+
+def test_router_ref_against_numpy(moe, layer, orc):
+    """or_router_ref against numpy's float64 x @ W.T on a slice of configuration 1 (F16
+    activations, F32 router weights [E, d])."""
+    cfg = layer.CONFIGS[1]
+    inp = layer.make_inputs(cfg, with_experts=False)
+    x = inp.x[:48]
+    w = inp.w_router
+    got = orc.router_ref(x, w)
+    ref = x.view(np.float16).astype(np.float64) @ w.astype(np.float64).T
+    assert got.shape == (48, cfg.n_experts)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-15)
+    # transposed roles (W rows against x columns) or a dropped last K term would not pass
+    short = x.view(np.float16).astype(np.float64)[:, :-1] @ w.astype(np.float64)[:, :-1].T
+    assert not np.allclose(got, short, rtol=1e-12, atol=1e-15)

@@ -70,3 +70,22 @@ def test_invalid_ids_counted_and_dropped(orc):
     g = orc.grouping(ids, E)
     flat = ids.reshape(-1)
     assert orc.plan_fields(g["plan"])["bad"] == int(((flat < 0) | (flat >= E)).sum()) > 0
+
+
+@pytest.mark.parametrize("E", [16, 512])
+@pytest.mark.parametrize("pattern", rp.PATTERNS)
+def test_gather_is_row_indexing(orc, pattern, E):
+    """or_gather against numpy fancy indexing x[src[:n_valid]], bit for bit, on the reference's id
+    patterns (pf_sort_eq_host_grouping.mm:462-480 checks Xs[a] == mixed_h[src[a]])."""
+    T, d = 300, 256
+    rng = np.random.default_rng(E)
+    x = rng.integers(0, 1 << 16, size=(T, d), dtype=np.uint16)
+    ids = rp.grouping_ids(T, E, pattern)
+    g = orc.grouping(ids, E)
+    n_valid = ids.size - orc.plan_fields(g["plan"])["bad"]
+    xs = orc.gather(x, g["src"], n_valid)
+    assert xs.shape == (n_valid, d)
+    assert np.array_equal(xs, x[g["src"][:n_valid]])
+    # a planted off-by-one in the source rows is caught by the same comparison
+    shifted = np.where(g["src"][:n_valid] + 1 < T, g["src"][:n_valid] + 1, 0).astype(np.int32)
+    assert not np.array_equal(orc.gather(x, shifted, n_valid), x[g["src"][:n_valid]])
