@@ -339,6 +339,18 @@ sm_status sm_submit_dequant(sm_context* ctx, void* stream, sm_format fmt, uint32
 sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b,
                                char* err, size_t cap);
+/* The full-mode layer (as sm_submit_full_layer) with its workspace in the library's fixed
+ * per-GPU scratch instead of caller views. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc); it allocates nothing. b->route_gather.histogram,
+ * b->gate_up.weights.address_snapshot and b->down.weights.address_snapshot must be null views:
+ * the histogram ((ceil(T*k/256) + 1) * E * 4 bytes, at most SM_FIXED_SCRATCH_HISTOGRAM_BYTES,
+ * else SM_E_SHAPE) and both snapshots live in the scratch. Every call on a GPU uses that GPU's
+ * one copy, so calls that overlap on one GPU race; calls ordered on one stream do not. */
+#define SM_FIXED_SCRATCH_HISTOGRAM_BYTES (1u << 20)
+sm_status sm_submit_full_layer_fixed_scratch(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                                             const sm_layer_formats* formats, const sm_layer_buffers* b,
+                                             char* err, size_t cap);
 sm_status sm_submit_prefill_moe_chunks(sm_context* ctx, void* stream, const sm_chunk_schedule* schedule,
                                        const sm_moe_shape* shape, const sm_layer_formats* formats,
                                        sm_view input, sm_view output, const sm_layer_buffers* b, char* err,

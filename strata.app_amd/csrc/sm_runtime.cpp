@@ -46,12 +46,44 @@ struct sm_context {
     hipStream_t side = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     std::mutex side_mu;
+    uintptr_t fixed_scratch = 0;  // this device's copy of the fixed scratch array (0: none)
 };
 
 namespace {
 // Handles are unique across every context of the process, so a view from another context
 // never resolves in this one's registry (the reference's "owned by this Context" check).
 std::atomic<uint64_t> g_next_handle{1};
+
+// ---- fixed scratch of sm_submit_full_layer_fixed_scratch ----------------------------------
+// The workspace of the allocation-free full layer lives in this array, one copy per GPU in
+// the code object's device globals: the grouping histogram (kFixedHistBytes), then the gate/up
+// and the down address snapshots (kFixedSnapBytes each). Host code never takes the array's
+// name as an address (on the host it is only a stand-in for the symbol): each device's copy
+// is resolved once, with that device current, by hipGetSymbolAddress, and that pointer is
+// what the kernels receive.
+constexpr uint64_t kFixedHistBytes = SM_FIXED_SCRATCH_HISTOGRAM_BYTES;
+constexpr uint64_t kFixedSnapBytes = 3ull * SM_MAX_EXPERTS * 8;
+static __device__ __align__(256) uint8_t scratch[kFixedHistBytes + 2 * kFixedSnapBytes];
+
+std::mutex g_scratch_mu;
+std::map<int, uintptr_t> g_scratch_ptr;  // device -> its copy of `scratch`
+
+// The device's copy of the fixed scratch (device current); 0 if it cannot be resolved.
+uintptr_t fixed_scratch_of(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(device);
+    if (it != g_scratch_ptr.end()) return it->second;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return 0;
+    g_scratch_ptr[device] = reinterpret_cast<uintptr_t>(p);
+    return reinterpret_cast<uintptr_t>(p);
+}
+
+// Where the allocation-free layer's workspace lies (all 0 on a context without a device,
+// which still validates).
+struct FixedScratch {
+    uintptr_t hist = 0, snap_gu = 0, snap_dn = 0;
+};
 }  // namespace
 
 struct sm_segment {
@@ -129,6 +161,7 @@ struct Check {
     sm_context* ctx;
     std::string prefix;  // e.g. "Prefill MoE grouping"
     int stage = 0;
+    const FixedScratch* fixed = nullptr;  // the histogram and snapshots come from the fixed scratch
     std::vector<Range> inputs, outputs;
     std::string err;
     sm_status st = SM_OK;
@@ -246,6 +279,20 @@ void encode_route_launch(sm_segment* seg, const sm_moe_shape& s, int divide, con
 }
 
 struct GroupRes { uintptr_t ids, mixed, hist, plan, tiles, src, dst, gathered; };
+
+// The grouping histogram: the caller's view, or the fixed scratch (its view must then be null).
+bool hist_view(Check& c, const sm_view& v, uint64_t bytes, uintptr_t& out) {
+    if (c.fixed == nullptr) return c.view(v, bytes, 4, "histogram", true, out);
+    if (v.buffer != 0) return c.fail(SM_E_ARGUMENT, c.prefix + " histogram view must be null: the fixed scratch holds it");
+    if (bytes > kFixedHistBytes) {
+        char msg[160];
+        std::snprintf(msg, sizeof msg, " histogram needs %llu bytes, more than the fixed scratch's %llu",
+                      (unsigned long long)bytes, (unsigned long long)kFixedHistBytes);
+        return c.fail(SM_E_SHAPE, c.prefix + msg);
+    }
+    out = c.fixed->hist;
+    return true;
+}
 bool check_grouping(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& b, GroupRes& r) {
     const uint64_t N = uint64_t(s.rows) * s.top_k;
     if (N > 0x7fffffffull) return c.fail(SM_E_SHAPE, c.prefix + " entry count exceeds kernel indexing");
@@ -256,7 +303,7 @@ bool check_grouping(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& 
         return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
     return c.view(b.ids, route_b, 4, "route IDs", false, r.ids) &&
            c.view(b.mixed_h, mixed_b, 16, "mixed activation", false, r.mixed) &&
-           c.view(b.histogram, hist_b, 4, "histogram", true, r.hist) &&
+           hist_view(c, b.histogram, hist_b, r.hist) &&
            c.view(b.plan, SM_PLAN_SLOT_BYTES, 4, "PfPlan slot", true, r.plan) &&
            c.view(b.tiles, tiles_b, 8, "tile list", true, r.tiles) &&
            c.view(b.source_rows, route_b, 4, "source rows", true, r.src) &&
@@ -318,7 +365,13 @@ bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, 
     if (w.layer >= w.n_layers)
         return c.fail(SM_E_ARGUMENT, c.prefix + " layer is outside the address table");
     const uint64_t E = s.n_experts;
-    if (!c.view(w.address_snapshot, E * 3 * 8, 8, "address snapshot", true, r.snapshot)) return false;
+    if (c.fixed != nullptr) {
+        if (w.address_snapshot.buffer != 0)
+            return c.fail(SM_E_ARGUMENT, c.prefix + " address snapshot view must be null: the fixed scratch holds it");
+        r.snapshot = gate_up ? c.fixed->snap_gu : c.fixed->snap_dn;
+    } else if (!c.view(w.address_snapshot, E * 3 * 8, 8, "address snapshot", true, r.snapshot)) {
+        return false;
+    }
     const uint64_t per_row = gate_up ? fmt_row_bytes(fmt, s.hidden) : fmt_row_bytes(fmt, s.expert_ff);
     uint64_t expert_bytes;
     if (!mul_ok({per_row, gate_up ? uint64_t(s.expert_ff) : uint64_t(s.hidden)}, expert_bytes) || per_row == 0)
@@ -749,6 +802,7 @@ sm_status sm_context_create(int device, sm_context** out) {
         ok = ok && hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) == hipSuccess &&
              hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming) == hipSuccess &&
              hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming) == hipSuccess;
+        if (ok) c->fixed_scratch = fixed_scratch_of(device);  // device is current here
         if (!ok) {
             sm_context_destroy(c);
             return SM_E_DEVICE;
@@ -1108,7 +1162,7 @@ static size_t shared_fork_offset(const sm_moe_shape& s) { return s.rows >= 8192 
 
 namespace {
 sm_status encode_full_layer_impl(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
-                                 const sm_layer_buffers* b, ChunkCtl* ctl) {
+                                 const sm_layer_buffers* b, ChunkCtl* ctl, const FixedScratch* fixed = nullptr) {
     const char* P = "full-mode Prefill MoE";
     if (seg == nullptr) return SM_E_ARGUMENT;
     if (seg->failed) return SM_E_SEGMENT;
@@ -1120,7 +1174,7 @@ sm_status encode_full_layer_impl(sm_segment* seg, const sm_moe_shape* shape, con
     const bool has_shared = s.shared_ff != 0;
     // Validate every stage before anything is recorded.
     Check cr, cs, cg, cd, cc;
-    for (Check* c : {&cr, &cs, &cg, &cd, &cc}) { c->ctx = seg->ctx; c->prefix = P; }
+    for (Check* c : {&cr, &cs, &cg, &cd, &cc}) { c->ctx = seg->ctx; c->prefix = P; c->fixed = fixed; }
     cr.stage = 0; cs.stage = 1; cg.stage = 2; cd.stage = 3; cc.stage = 4;
     RouterRes rr{};
     RouteRes ro{};
@@ -1336,6 +1390,38 @@ sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape
                                const sm_layer_formats* formats, const sm_layer_buffers* b, char* err,
                                size_t cap) {
     SM_SUBMIT_BODY(sm_encode_full_layer(seg, shape, formats, b))
+}
+
+sm_status sm_submit_full_layer_fixed_scratch(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                                             const sm_layer_formats* formats, const sm_layer_buffers* b, char* err,
+                                             size_t cap) {
+    auto message = [&](const char* msg) {
+        if (err && cap) std::snprintf(err, cap, "%s", msg);
+    };
+    if (ctx == nullptr) return SM_E_ARGUMENT;
+    FixedScratch fs;
+    if (ctx->fixed_scratch != 0) {
+        fs.hist = ctx->fixed_scratch;
+        fs.snap_gu = fs.hist + kFixedHistBytes;
+        fs.snap_dn = fs.snap_gu + kFixedSnapBytes;
+    }
+    sm_segment* seg = nullptr;
+    sm_status st = sm_segment_begin(ctx, &seg);
+    if (st != SM_OK) return st;
+    st = encode_full_layer_impl(seg, shape, formats, b, nullptr, &fs);
+    if (st != SM_OK) {
+        message(seg->error.c_str());
+        sm_segment_abort(seg);
+        return st;
+    }
+    if (ctx->fixed_scratch == 0) {  // validated, but there is no device copy to run on
+        message("full-mode Prefill MoE fixed scratch is not available on this context's device");
+        sm_segment_abort(seg);
+        return SM_E_DEVICE;
+    }
+    st = sm_segment_commit(seg, stream);
+    message(st != SM_OK ? "HIP launch failed" : "");
+    return st;
 }
 
 sm_status sm_submit_prefill_moe_chunks(sm_context* ctx, void* stream, const sm_chunk_schedule* schedule,

@@ -44,7 +44,7 @@ EXPORTS = (
     "sm_submit_gate_up", "sm_submit_down", "sm_submit_swiglu", "sm_submit_combine",
     "sm_submit_full_layer", "sm_read_layer_status",
     "sm_build_chunk_schedule", "sm_chunk_count", "sm_chunk_range_at", "sm_encode_prefill_moe_chunks",
-    "sm_submit_prefill_moe_chunks",
+    "sm_submit_prefill_moe_chunks", "sm_submit_full_layer_fixed_scratch",
     "sm_synth_normal_f32", "sm_synth_normal_f16", "sm_synth_normal_bf16", "sm_quantize",
     "sm_synth_quantized",
 )
@@ -184,6 +184,8 @@ def library() -> C.CDLL:
         "sm_chunk_range_at": (I, [C.POINTER(ChunkSchedule), U64, C.POINTER(ChunkRange)]),
         "sm_encode_prefill_moe_chunks": (I, [P, C.POINTER(ChunkSchedule), C.POINTER(Shape), C.POINTER(LayerFormats),
                                              View, View, C.POINTER(LayerBuffers)]),
+        "sm_submit_full_layer_fixed_scratch": (I, [P, P, C.POINTER(Shape), C.POINTER(LayerFormats),
+                                                   C.POINTER(LayerBuffers), C.c_char_p, C.c_size_t]),
         "sm_submit_prefill_moe_chunks": (I, [P, P, C.POINTER(ChunkSchedule), C.POINTER(Shape),
                                              C.POINTER(LayerFormats), View, View, C.POINTER(LayerBuffers),
                                              C.c_char_p, C.c_size_t]),
