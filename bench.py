@@ -72,30 +72,38 @@ def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: boo
     t0 = time.time()
     inp = layer.make_inputs(cfg)
     log(f"inputs ready in {time.time() - t0:.1f}s; uploading")
-    chunks = [layer.LayerWorkspace(ctx, cfg, inp, chunk=c) for c in range(cfg.chunks)]
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+    # A multi-chunk prompt runs through the chunk driver: every chunk in one segment, one set of
+    # chunk scratch. The timed step encodes + validates + commits the whole prompt.
+    if cfg.chunks > 1:
+        pw = layer.PromptWorkspace(ctx, cfg, inp)
+        ws = pw.chunk
 
-    # Pre-encoded buffer structs: the timed loop encodes + validates + commits each step.
-    lbs = [ws.layer_buffers() for ws in chunks]
+        def encode(seg):
+            return pw.encode(seg)
+    else:
+        ws = layer.LayerWorkspace(ctx, cfg, inp)
+        lb = ws.layer_buffers()
+
+        def encode(seg):
+            return seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, lb)
 
     def step():
-        for ws, lb in zip(chunks, lbs):
-            seg = ctx.segment()
-            ok, err = seg.encode_prefill_moe_full_mode_layer(ws.shape, ws.formats, lb)
-            if not ok:
-                seg.abort()
-                raise RuntimeError(err)
-            seg.commit(sh)
+        seg = ctx.segment()
+        ok, err = encode(seg)
+        if not ok:
+            seg.abort()
+            raise RuntimeError(err)
+        seg.commit(sh)
 
     log("warmup")
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    for ws in chunks:
-        st = ws.read_status(sh)
-        if st != (0, 0, 0):
-            raise RuntimeError(f"layer status {st}")
+    st = ws.read_status(sh)
+    if st != (0, 0, 0):
+        raise RuntimeError(f"layer status {st}")
     log(f"timing {steps} steps")
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -108,7 +116,6 @@ def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: boo
     value = T * cfg.chunks / (ms_per_step / 1e3)
     log(f"{ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
 
-    ws = chunks[0]
     reps = max(5, steps)
 
     def stage_ms(encode):
@@ -165,6 +172,62 @@ def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: boo
         "gu_bytes": n_groups * 2 * I * gu_row + N * d * 2 + N * I * 2, "gu_flops": 2.0 * N * 2 * I * d,
         "dn_bytes": n_groups * d * dn_row + N * I * 2 + N * d * 4, "dn_flops": 2.0 * N * d * I,
     }
+
+
+def measure_route(moe, layer, ctx, steps: int):
+    """Configuration 1 (T=4096, routing + grouping + gather only): each launch of the
+    route/gather stage alone, with HIP events around it on the caller's stream."""
+    import torch
+    cfg = layer.CONFIGS[1]
+    T, d, E, K = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k
+    N = T * K
+    log("config 1 (route_group): generating inputs")
+    ws = layer.LayerWorkspace(ctx, cfg, layer.make_inputs(cfg, with_experts=False))
+    sh = torch.cuda.current_stream().cuda_stream
+    rg = ws.route_gather_buffers()
+    acc = {}
+    for i in range(max(5, steps) + 2):
+        seg = ctx.segment()
+        ok, err = seg.encode_prefill_moe_full_mode_route_gather(ws.shape, rg)
+        assert ok, err
+        for label, ms in seg.commit_timed(sh):
+            if i >= 2:
+                acc.setdefault(label, []).append(ms)
+    us = {k: sum(v) / len(v) * 1e3 for k, v in acc.items()}
+    router_flops = 2.0 * T * E * d
+    topk_bytes = T * E * 4 + N * 8
+    gather_bytes = N * d * 2 + T * d * 2 + N * 4
+    out = {
+        "workload": "config1:route_group", "tokens": T,
+        "router_gemm": {"kernel_us": round(us["router GEMM"], 2),
+                        "tflops": round(router_flops / us["router GEMM"] / 1e6, 1)},
+        "top_k": {"kernel_us": round(us["route top-k"], 2),
+                  "gbs": round(topk_bytes / us["route top-k"] / 1e3, 1)},
+        "grouping": {"kernel_us": round(us["grouping"], 2)},
+        "gather": {"kernel_us": round(us["gather"], 2), "gbs": round(gather_bytes / us["gather"] / 1e3, 1),
+                   "frac": round(gather_bytes / us["gather"] / 1e3 / HBM_PEAK_GBS, 4)},
+        "stage_us": round(sum(us.values()), 2),
+    }
+    log(f"config 1: {out}")
+    return out
+
+
+def cpu_description() -> dict:
+    """The host the CPU baseline ran on: model name, logical CPUs, NUMA nodes."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    numa = None
+    try:
+        numa = Path("/sys/devices/system/node/online").read_text().strip()
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "numa_nodes_online": numa}
 
 
 def main() -> int:
@@ -244,7 +307,7 @@ def main() -> int:
     }
     # ---- the T >= 8192 figures the metric names: configuration 3 (Zipf-skewed) ----
     if args.config == 2 and not args.no_config3:
-        m3 = measure(moe, layer, ctx, 3, max(3, args.steps // 4), 2, detailed=False)
+        m3 = measure(moe, layer, ctx, 3, max(20, args.steps), 3, detailed=False)
         g3 = m3["gu_flops"] / (m3["gu_kernel_ms"] / 1e3) / 1e12
         d3 = m3["dn_flops"] / (m3["dn_kernel_ms"] / 1e3) / 1e12
         extra["config3"] = {
@@ -257,25 +320,49 @@ def main() -> int:
                      "gbs": round(m3["dn_bytes"] / (m3["dn_kernel_ms"] / 1e3) / 1e9, 1)},
         }
         log(f"config 3: {extra['config3']}")
+    # ---- the routing-only configuration (1) and the low-bit 4 x 4096 prompt (4) ----
+    if args.config == 2 and not args.no_config3:
+        extra["config1"] = measure_route(moe, layer, ctx, args.steps)
+        m4 = measure(moe, layer, ctx, 4, max(10, args.steps // 2), 3, detailed=False)
+        g4 = m4["gu_flops"] / (m4["gu_kernel_ms"] / 1e3) / 1e12
+        d4 = m4["dn_flops"] / (m4["dn_kernel_ms"] / 1e3) / 1e12
+        extra["config4"] = {
+            "workload": "config4:low_bit (16384 tokens as 4 chunks of 4096, chunk driver)",
+            "tokens": m4["cfg"].rows * m4["cfg"].chunks, "ms_per_step": round(m4["ms_per_step"], 4),
+            "tokens_per_s": round(m4["value"], 1),
+            "layer_tflops": round(layer.layer_flops(m4["cfg"]) * m4["cfg"].chunks / (m4["ms_per_step"] / 1e3) / 1e12, 1),
+            "gate_up_chunk": {"kernel_us": round(m4["gu_kernel_ms"] * 1e3, 2), "tflops": round(g4, 1),
+                              "mfma_frac": round(g4 / F16_MFMA_PEAK_TFLOPS, 4)},
+            "down_chunk": {"kernel_us": round(m4["dn_kernel_ms"] * 1e3, 2), "tflops": round(d4, 1),
+                           "mfma_frac": round(d4 / F16_MFMA_PEAK_TFLOPS, 4)},
+        }
+        log(f"config 4: {extra['config4']}")
 
     # ---- CPU baseline: the C++ restatement of the same stages on a bounded sample ----
     cpu = None
     if not args.no_cpu:
         orc = ge.load_oracle()
-        log("cpu baseline")
-        _, st, threads = orc.cpu_layer(cfg, inp, n_threads=args.cpu_threads)  # warm-up
-        times = []
+        # Built here for this host's own instruction set (-march=native); the portable build
+        # is the fallback.
+        arch = "native" if orc.build_native() else "x86-64-v3"
+        log(f"cpu baseline ({arch} build)")
+        _, st0, threads = orc.cpu_layer(cfg, inp, n_threads=args.cpu_threads, native=arch == "native")  # warm-up
+        times, stages_runs = [], []
         t_budget = time.time()
-        while len(times) < 3 and (time.time() - t_budget) < 30.0:
+        while len(times) < 5 or (len(times) < 9 and time.time() - t_budget < 20.0):
             a = time.perf_counter()
-            orc.cpu_layer(cfg, inp, n_threads=args.cpu_threads)
+            _, st, _ = orc.cpu_layer(cfg, inp, n_threads=args.cpu_threads, native=arch == "native")
             times.append(time.perf_counter() - a)
+            stages_runs.append(st)
         med = sorted(times)[len(times) // 2]
+        names = ["router", "top_k", "grouping_gather", "shared_ffn", "gate_up", "down", "combine"]
+        stage_med = {k: round(float(sorted(r[i] for r in stages_runs)[len(stages_runs) // 2]), 1)
+                     for i, k in enumerate(names)}
         cpu = {"value": round(T / med, 1), "unit": "tokens/s", "cores": int(threads), "kind": "port",
-               "sample": f"{len(times)} timed call(s) of one {T}-token chunk of configuration {args.config} "
+               "sample": f"median of {len(times)} timed calls of one {T}-token chunk of configuration {args.config} "
                          f"(all stages, median {med:.3f}s) after one warm-up call",
-               "stage_us": {k: round(float(v), 1) for k, v in zip(
-                   ["router", "top_k", "grouping_gather", "shared_ffn", "gate_up", "down", "combine"], st)}}
+               "build": f"g++ -O3 -march={arch} -fopenmp", "host": cpu_description(),
+               "stage_us": stage_med}
         log(f"cpu baseline {cpu['value']} tokens/s on {threads} threads")
 
     line = {

@@ -13,8 +13,10 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle_moe.so"
+NATIVE_LIB = HERE / "_native" / "liboracle_moe.so"
 REF_LIB = HERE / "_ref" / "libref_twins.so"
 _lib = None
+_native = None
 _ref = None
 P = C.c_void_p
 
@@ -26,34 +28,49 @@ def build(reference_root: str = "/root/reference") -> None:
         subprocess.run([str(HERE / "build_ref.sh"), reference_root], check=True)
 
 
-def lib() -> C.CDLL:
-    global _lib
+def build_native() -> bool:
+    """Builds oracle/_native/liboracle_moe.so for this host's instruction set (-march=native),
+    where the CPU baseline is timed; False if the build fails (the portable library is used)."""
+    res = subprocess.run(["make", "-s", "-C", str(HERE), "native"], capture_output=True, text=True)
+    return res.returncode == 0 and NATIVE_LIB.exists()
+
+
+def lib(native: bool = False) -> C.CDLL:
+    global _lib, _native
+    if native:
+        if _native is None:
+            _native = _bind(C.CDLL(str(NATIVE_LIB)))
+        return _native
     if _lib is None:
         if not LIB.exists():
             build()
-        L = C.CDLL(str(LIB))
-        U32, U64, I, F = C.c_uint32, C.c_uint64, C.c_int, C.c_float
-        sig = {
-            "or_exp": (F, [F]), "or_f32_to_f16": (C.c_uint16, [F]), "or_f16_to_f32": (F, [C.c_uint16]),
-            "or_half_sat": (C.c_uint16, [F]), "or_silu": (F, [F]), "or_sigmoid": (F, [F]),
-            "or_row_bytes": (U64, [I, U64]), "or_dequant": (I, [I, P, U64, P]),
-            "or_route": (I, [P, U32, U32, U32, I, P, P]),
-            "or_grouping": (I, [P, U32, U32, U32, P, P, P, P, P, P]),
-            "or_gather": (I, [P, U32, U32, P, U32, P]),
-            "or_router_ref": (I, [P, P, U32, U32, U32, P]),
-            "or_gate_up_ref": (I, [I, P, U32, U32, P, P, P, U64, P, U32, P, P, P]),
-            "or_down_ref": (I, [I, P, U32, U32, P, P, U64, P, U32, P]),
-            "or_shared_ref": (I, [I, P, U32, U32, P, P, P, P, P, U32, P, P, P]),
-            "or_swiglu": (I, [P, P, U64, P]),
-            "or_combine": (I, [P, P, P, P, U32, U32, U32, P]),
-            "or_cpu_layer": (I, [U32, U32, U32, U32, U32, U32, I, I, I, P, P, P, P, U64, P, U64,
-                                 P, P, P, P, I, P, P]),
-        }
-        for n, (r, a) in sig.items():
-            f = getattr(L, n)
-            f.restype, f.argtypes = r, a
-        _lib = L
+        _lib = _bind(C.CDLL(str(LIB)))
     return _lib
+
+
+def _bind(L: C.CDLL) -> C.CDLL:
+    """Declares the oracle library's signatures."""
+    U32, U64, I, F = C.c_uint32, C.c_uint64, C.c_int, C.c_float
+    sig = {
+        "or_exp": (F, [F]), "or_f32_to_f16": (C.c_uint16, [F]), "or_f16_to_f32": (F, [C.c_uint16]),
+        "or_half_sat": (C.c_uint16, [F]), "or_silu": (F, [F]), "or_sigmoid": (F, [F]),
+        "or_row_bytes": (U64, [I, U64]), "or_dequant": (I, [I, P, U64, P]),
+        "or_route": (I, [P, U32, U32, U32, I, P, P]),
+        "or_grouping": (I, [P, U32, U32, U32, P, P, P, P, P, P]),
+        "or_gather": (I, [P, U32, U32, P, U32, P]),
+        "or_router_ref": (I, [P, P, U32, U32, U32, P]),
+        "or_gate_up_ref": (I, [I, P, U32, U32, P, P, P, U64, P, U32, P, P, P]),
+        "or_down_ref": (I, [I, P, U32, U32, P, P, U64, P, U32, P]),
+        "or_shared_ref": (I, [I, P, U32, U32, P, P, P, P, P, U32, P, P, P]),
+        "or_swiglu": (I, [P, P, U64, P]),
+        "or_combine": (I, [P, P, P, P, U32, U32, U32, P]),
+        "or_cpu_layer": (I, [U32, U32, U32, U32, U32, U32, I, I, I, P, P, P, P, U64, P, U64,
+                             P, P, P, P, I, P, P]),
+    }
+    for n, (r, a) in sig.items():
+        f = getattr(L, n)
+        f.restype, f.argtypes = r, a
+    return L
 
 
 def ref() -> C.CDLL | None:
@@ -180,14 +197,14 @@ def combine(parts, weights, shared, gl, rows, top_k, d):
     return out
 
 
-def cpu_layer(cfg, inputs, n_threads: int = 0, chunk: int = 0):
+def cpu_layer(cfg, inputs, n_threads: int = 0, chunk: int = 0, native: bool = False):
     """Times the CPU restatement of one layer call; returns (out, stage_us, threads)."""
     T, d = cfg.rows, cfg.hidden
     x = np.ascontiguousarray(inputs.x[chunk * T:(chunk + 1) * T])
     out = np.empty((T, d), np.float32)
     st = np.zeros(7, np.float64)
     Is = cfg.shared_ff
-    th = lib().or_cpu_layer(T, d, cfg.n_experts, cfg.top_k, cfg.expert_ff, Is, cfg.gate_up_fmt, cfg.down_fmt,
+    th = lib(native).or_cpu_layer(T, d, cfg.n_experts, cfg.top_k, cfg.expert_ff, Is, cfg.gate_up_fmt, cfg.down_fmt,
                             cfg.shared_fmt, _p(x), _p(inputs.w_router), _p(inputs.w_gate), _p(inputs.w_up),
                             inputs.gu_stride, _p(inputs.w_down), inputs.dn_stride,
                             _p(inputs.sh_gate) if Is else None, _p(inputs.sh_up) if Is else None,
