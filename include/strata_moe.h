@@ -54,7 +54,8 @@ typedef enum sm_status {
     SM_E_SEGMENT = 6,   /* segment already failed / committed                               */
     SM_E_FORMAT = 7,    /* weight format not supported for this role                        */
     SM_E_ADDRESS = 8,   /* expert weight address outside declared storage or misaligned    */
-    SM_E_DEVICE = 9     /* HIP runtime error                                                */
+    SM_E_DEVICE = 9,    /* HIP runtime error                                                */
+    SM_E_FILE = 10      /* model file missing, truncated or malformed                       */
 } sm_status;
 
 /* Weight formats (ggml block layouts, third_party/ggml/ggml-common.h:252-338). */
@@ -355,6 +356,46 @@ sm_status sm_submit_prefill_moe_chunks(sm_context* ctx, void* stream, const sm_c
                                        const sm_moe_shape* shape, const sm_layer_formats* formats,
                                        sm_view input, sm_view output, const sm_layer_buffers* b, char* err,
                                        size_t cap);
+
+/* ---- model file: GGUF expert tensors -> device storage + address table ------------------ */
+/* The reference's full-mode layout (src/metal/engine/window.cpp:128-270): every layer's routed
+ * experts are the GGUF tensors blk.<l>.ffn_{gate,up,down}_exps.weight, ne = [d, I, E] for gate
+ * and up (one type) and [I, d, E] for down (docs/mac/03-model-reference.md:292-297), each
+ * expert a contiguous slab; the [layer][E][3] table holds each slab's device address. */
+typedef struct sm_gguf sm_gguf;
+typedef struct sm_gguf_tensor {
+    uint32_t ggml_type;      /* ggml type id (0 F32, 1 F16, 8 Q8_0, 10 Q2_K, 12 Q4_K, 30 BF16, ...) */
+    uint32_t n_dims;
+    uint64_t ne[4];          /* ne[0] varies fastest; unused dimensions are 1                  */
+    uint64_t offset;         /* absolute file offset of the data                               */
+    uint64_t bytes;          /* data bytes (0 for a type without a known block layout)         */
+} sm_gguf_tensor;
+#define SM_GGUF_MAX_LAYERS 64u
+typedef struct sm_expert_layout {
+    uint32_t n_layers, n_experts, hidden, expert_ff;
+    sm_format gate_up, down;
+    uint64_t total_bytes;                      /* device bytes for every expert tensor          */
+    uint64_t offsets[SM_GGUF_MAX_LAYERS][3];   /* each tensor's offset in that storage (256-aligned) */
+} sm_expert_layout;
+/* Opens a GGUF v2/v3 file and validates its header, metadata and tensor directory (every
+ * tensor's data inside the file, aligned to general.alignment). SM_E_FILE on a bad file. */
+sm_status sm_gguf_open(const char* path, sm_gguf** out, char* err, size_t cap);
+void sm_gguf_close(sm_gguf* gguf);
+uint64_t sm_gguf_tensor_count(const sm_gguf* gguf);
+/* SM_E_ARGUMENT when the tensor does not exist. */
+sm_status sm_gguf_find(const sm_gguf* gguf, const char* name, sm_gguf_tensor* out);
+/* The expert tensors of layers 0..n_layers-1: every one present, 3-D, Q8_0/Q4_K/Q2_K, shapes and
+ * types equal across layers, expert slabs aligned for the kernels; and where each goes in one
+ * device allocation of total_bytes. */
+sm_status sm_gguf_expert_layout(const sm_gguf* gguf, uint32_t n_layers, sm_expert_layout* out, char* err,
+                                size_t cap);
+/* Copies every expert tensor of `layout` from the file into `storage` (a registered device view
+ * of at least layout->total_bytes, 256-byte aligned) through pinned chunks on `stream`, waits
+ * for the copies, and writes the host [n_layers][E][3] address table (n_addresses >=
+ * n_layers * E * 3) for sm_expert_weights.addresses (with n_layers and the selected layer). */
+sm_status sm_gguf_load_experts(sm_gguf* gguf, sm_context* ctx, void* stream, const sm_expert_layout* layout,
+                               sm_view storage, uint64_t* addresses, uint64_t n_addresses, char* err,
+                               size_t cap);
 
 /* ---- after completion ----------------------------------------------------------------- */
 /* Synchronises `stream`, then reads the plan's `bad` count and up to two status words

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../include/strata_moe.h"
+#include "sm_internal.h"
 #include "sm_launch.h"
 
 struct sm_context {
@@ -768,6 +769,22 @@ bool expected_edge(const Range& w, const Range& r) {
 extern "C" {
 
 uint32_t sm_abi_version(void) { return SM_ABI_VERSION; }
+
+sm_status sm_internal_resolve_view(sm_context* ctx, sm_view v, uint64_t need, uint64_t align, uintptr_t* out) {
+    if (!ctx || !out || align == 0) return SM_E_ARGUMENT;
+    sm_context::Alloc a{};
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        auto it = ctx->buffers.find(v.buffer);
+        if (v.buffer == 0 || it == ctx->buffers.end()) return SM_E_OWNERSHIP;
+        a = it->second;
+    }
+    const uint64_t end = v.offset + v.length;
+    const uintptr_t p = a.ptr + v.offset;
+    if (end < v.offset || end > a.bytes || v.length < need || p % align != 0) return SM_E_VIEW;
+    *out = p;
+    return SM_OK;
+}
 
 uint64_t sm_histogram_bytes(const sm_moe_shape* s) {
     if (!s) return 0;

@@ -24,7 +24,7 @@ Q8_0, Q4_K, Q2_K, F16, BF16 = 1, 2, 3, 4, 5
 FORMAT_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q2_K: "Q2_K", F16: "F16", BF16: "BF16"}
 STATUS_NAMES = {
     0: "SM_OK", 1: "SM_E_ARGUMENT", 2: "SM_E_SHAPE", 3: "SM_E_VIEW", 4: "SM_E_OWNERSHIP",
-    5: "SM_E_ALIAS", 6: "SM_E_SEGMENT", 7: "SM_E_FORMAT", 8: "SM_E_ADDRESS", 9: "SM_E_DEVICE",
+    5: "SM_E_ALIAS", 6: "SM_E_SEGMENT", 7: "SM_E_FORMAT", 8: "SM_E_ADDRESS", 9: "SM_E_DEVICE", 10: "SM_E_FILE",
 }
 PLAN_BYTES = 6180
 PLAN_SLOT_BYTES = 6400
@@ -45,6 +45,8 @@ EXPORTS = (
     "sm_submit_full_layer", "sm_read_layer_status",
     "sm_build_chunk_schedule", "sm_chunk_count", "sm_chunk_range_at", "sm_encode_prefill_moe_chunks",
     "sm_submit_prefill_moe_chunks", "sm_submit_full_layer_fixed_scratch",
+    "sm_gguf_open", "sm_gguf_close", "sm_gguf_tensor_count", "sm_gguf_find", "sm_gguf_expert_layout",
+    "sm_gguf_load_experts",
     "sm_synth_normal_f32", "sm_synth_normal_f16", "sm_synth_normal_bf16", "sm_quantize",
     "sm_synth_quantized",
 )
@@ -119,6 +121,20 @@ class LayerBuffers(C.Structure):
                 ("combine", CombineBuffers)]
 
 
+class GgufTensor(C.Structure):
+    _fields_ = [("ggml_type", C.c_uint32), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4), ("offset", C.c_uint64),
+                ("bytes", C.c_uint64)]
+
+
+GGUF_MAX_LAYERS = 64
+
+
+class ExpertLayout(C.Structure):
+    _fields_ = [("n_layers", C.c_uint32), ("n_experts", C.c_uint32), ("hidden", C.c_uint32), ("expert_ff", C.c_uint32),
+                ("gate_up", C.c_int), ("down", C.c_int), ("total_bytes", C.c_uint64),
+                ("offsets", (C.c_uint64 * 3) * GGUF_MAX_LAYERS)]
+
+
 class ChunkSchedule(C.Structure):
     """PrefillChunkSchedule (include/strata/metal/prefill.hpp:47-72)."""
     _fields_ = [("pos0", C.c_uint32), ("chunk_rows", C.c_uint32), ("token_count", C.c_uint64)]
@@ -179,6 +195,13 @@ def library() -> C.CDLL:
                                      C.POINTER(LayerBuffers), C.c_char_p, C.c_size_t]),
         "sm_read_layer_status": (I, [P, P, View, View, View, C.POINTER(U32), C.POINTER(U32),
                                      C.POINTER(U32)]),
+        "sm_gguf_open": (I, [C.c_char_p, C.POINTER(P), C.c_char_p, C.c_size_t]),
+        "sm_gguf_close": (None, [P]),
+        "sm_gguf_tensor_count": (U64, [P]),
+        "sm_gguf_find": (I, [P, C.c_char_p, C.POINTER(GgufTensor)]),
+        "sm_gguf_expert_layout": (I, [P, U32, C.POINTER(ExpertLayout), C.c_char_p, C.c_size_t]),
+        "sm_gguf_load_experts": (I, [P, P, P, C.POINTER(ExpertLayout), View, C.POINTER(C.c_uint64), U64, C.c_char_p,
+                                     C.c_size_t]),
         "sm_build_chunk_schedule": (I, [U32, U64, U32, C.POINTER(ChunkSchedule), C.c_char_p, C.c_size_t]),
         "sm_chunk_count": (U64, [C.POINTER(ChunkSchedule)]),
         "sm_chunk_range_at": (I, [C.POINTER(ChunkSchedule), U64, C.POINTER(ChunkRange)]),
@@ -311,6 +334,59 @@ class ExpertTable:
         self._storage = (View * max(1, len(storage)))(*storage)
         self.struct = ExpertWeights(C.cast(self._addr, C.POINTER(C.c_uint64)), n_layers, layer, snapshot,
                                     C.cast(self._storage, C.POINTER(View)), len(storage))
+
+
+class GgufFile:
+    """A GGUF model file: its tensor directory and the routed-expert layout (sm_gguf_*)."""
+
+    def __init__(self, path):
+        self.lib = library()
+        h = C.c_void_p()
+        err = C.create_string_buffer(512)
+        self.status = self.lib.sm_gguf_open(str(path).encode(), C.byref(h), err, 512)
+        self.error = err.value.decode()
+        self.handle = h if self.status == 0 else None
+
+    def __bool__(self):
+        return self.handle is not None
+
+    def tensor_count(self) -> int:
+        return int(self.lib.sm_gguf_tensor_count(self.handle))
+
+    def find(self, name: str):
+        t = GgufTensor()
+        if self.lib.sm_gguf_find(self.handle, name.encode(), C.byref(t)) != 0:
+            return None
+        return dict(type=t.ggml_type, ne=tuple(t.ne[: t.n_dims]), offset=t.offset, bytes=t.bytes)
+
+    def expert_layout(self, n_layers: int):
+        """(ExpertLayout, "") or (None, message)."""
+        out = ExpertLayout()
+        err = C.create_string_buffer(512)
+        st = self.lib.sm_gguf_expert_layout(self.handle, n_layers, C.byref(out), err, 512)
+        return (out, "") if st == 0 else (None, f"{STATUS_NAMES.get(st, st)}: {err.value.decode()}")
+
+    def load_experts(self, ctx: "Context", stream, layout: ExpertLayout, storage: View):
+        """Copies the expert tensors into `storage`; returns the [n_layers * E * 3] address list."""
+        n = layout.n_layers * layout.n_experts * 3
+        table = (C.c_uint64 * n)()
+        err = C.create_string_buffer(512)
+        st = self.lib.sm_gguf_load_experts(self.handle, ctx.handle, C.c_void_p(stream), C.byref(layout), storage,
+                                           table, n, err, 512)
+        if st != 0:
+            raise RuntimeError(f"sm_gguf_load_experts: {STATUS_NAMES.get(st, st)}: {err.value.decode()}")
+        return list(table)
+
+    def close(self):
+        if self.handle:
+            self.lib.sm_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def build_chunk_schedule(pos0: int, token_count: int, chunk_rows: int):
