@@ -147,6 +147,8 @@ typedef struct sm_grouping_buffers {
     sm_view source_rows;      /* I32 [T*k]: grouped entry -> token                        */
     sm_view destination_rows; /* I32 [T*k]: grouped entry -> route index t*k+r            */
     sm_view gathered_rows;    /* F16 [T*k,d]                                              */
+    sm_view resident;         /* I32 [layer][E] residency table (tiered mode); null = all resident */
+    uint32_t layer;           /* the layer's row of `resident`                             */
 } sm_grouping_buffers;
 
 /* PrefillMoeRouteGatherBuffers (prefill_moe_pipeline.hpp:21-33): router GEMM + top-k +
@@ -164,6 +166,8 @@ typedef struct sm_route_gather_buffers {
     sm_view destination_rows;
     sm_view gathered_rows;
     sm_view router_bias;      /* F32 [E] added to the logits; null view = none            */
+    sm_view resident;         /* as in sm_grouping_buffers                                 */
+    uint32_t layer;
 } sm_route_gather_buffers;
 
 /* Routed expert weights: a host copy of the model's [layer][E][3] device-address table
@@ -172,6 +176,7 @@ typedef struct sm_route_gather_buffers {
  * argument does (prefill_moe_expert_dispatch.mm:259-266); that row is validated against the
  * declared storage views (prefill_moe_expert_dispatch.mm:377-448) and copied at commit into
  * `address_snapshot` (device, E*3*8 bytes) before the kernels. */
+typedef struct sm_lease_set sm_lease_set;
 typedef struct sm_expert_weights {
     const uint64_t* addresses;
     uint32_t n_layers;          /* rows of `addresses` (layer < n_layers)                   */
@@ -179,6 +184,11 @@ typedef struct sm_expert_weights {
     sm_view address_snapshot;
     const sm_view* storage;
     uint32_t n_storage;
+    /* Tiered mode (prefill_moe_expert_dispatch.hpp:36-37): addresses inside `slot_arena` are
+     * expert-store slots and must be pinned by `leases` for `layer`; an unpinned one makes the
+     * kernels report status bit 2 for that expert and zero its rows. Null view / NULL = none. */
+    sm_view slot_arena;
+    const sm_lease_set* leases;
 } sm_expert_weights;
 
 /* PrefillMoeExpertTileBuffers (prefill_moe_expert_dispatch.hpp:20-51). */
@@ -396,6 +406,46 @@ sm_status sm_gguf_expert_layout(const sm_gguf* gguf, uint32_t n_layers, sm_exper
 sm_status sm_gguf_load_experts(sm_gguf* gguf, sm_context* ctx, void* stream, const sm_expert_layout* layout,
                                sm_view storage, uint64_t* addresses, uint64_t n_addresses, char* err,
                                size_t cap);
+
+/* ---- tiered residency: expert store, slot leases and the per-layer handshake ------------- */
+/* The reference's ExpertStore / ExpertLeaseSet (include/strata/metal/experts.hpp:18-90) and the
+ * layer handshake (docs/mac/06-engine-host-port.md section 9.3): when the experts do not all
+ * fit in HBM, the grouping marks each group resident or not from the layer's residency-table
+ * row (PfPlan grp_res, n_miss, skip); the host then resolves the misses into slots of a device
+ * arena before the expert stages run. Here the handshake is host-driven between segments: the
+ * routing segment is committed, sm_expert_store_resolve_layer waits for it, reads the plan,
+ * brings each missing expert from the cold tier (the model's GGUF file) into a slot of half
+ * layer % 2 (least recently used unpinned slot, or a cached one), writes the slot addresses
+ * into the layer's address-table row and pins them in the lease set; then the expert segment is
+ * encoded with that table, the arena and the lease set. */
+typedef struct sm_expert_store sm_expert_store;
+typedef struct sm_store_stats {
+    uint64_t hits, lookups, file_reads, file_bytes;   /* ExpertLayerStats (experts.hpp:45-51) */
+} sm_store_stats;
+/* Bytes of one slot: the gate, up and down slabs of one expert, each 256-byte aligned. */
+uint64_t sm_expert_slot_bytes(const sm_expert_layout* layout);
+/* A store over the experts of `layout` in `gguf` (the cold tier) with `slot_arena` (a registered
+ * device view of at least 2 * slots_per_half * sm_expert_slot_bytes bytes) as two halves. */
+sm_status sm_expert_store_create(sm_context* ctx, sm_gguf* gguf, const sm_expert_layout* layout, sm_view slot_arena,
+                                 uint32_t slots_per_half, sm_expert_store** out, char* err, size_t cap);
+void sm_expert_store_destroy(sm_expert_store* store);
+/* A lease set for one command sequence (prepare_command_buffer): its pins keep slots from
+ * being reused until they are retired or the set is destroyed, which the caller does only
+ * after the GPU work that reads the slots has completed. */
+sm_status sm_lease_set_create(sm_expert_store* store, sm_lease_set** out);
+void sm_lease_set_destroy(sm_lease_set* leases);
+void sm_lease_set_retire_layer(sm_lease_set* leases, uint32_t layer);
+/* ExpertLeaseSet::pins (experts.hpp:30-31): 1 if a pin of `layer` covers [address, +bytes). */
+int sm_lease_set_pins(const sm_lease_set* leases, uint32_t layer, uint64_t address, uint64_t bytes);
+/* resolve_layer_after_plan (experts.hpp:74-85): waits for `stream` (the grouping that wrote
+ * `plan` is committed on it), retires the lease set's pins of earlier layers, reads the plan
+ * (only the header when skip is set; n_miss must match the groups marked non-resident), resolves
+ * every non-resident group's expert into a slot and writes its three slot addresses into
+ * table[(layer * E + e) * 3 + role] (n_table >= (layer + 1) * E * 3). On failure nothing of the
+ * layer is pinned and the table row may be partly written. */
+sm_status sm_expert_store_resolve_layer(sm_expert_store* store, void* stream, uint32_t layer, sm_view plan,
+                                        sm_lease_set* leases, uint64_t* table, uint64_t n_table,
+                                        sm_store_stats* stats, char* err, size_t cap);
 
 /* ---- after completion ----------------------------------------------------------------- */
 /* Synchronises `stream`, then reads the plan's `bad` count and up to two status words

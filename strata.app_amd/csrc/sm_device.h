@@ -81,6 +81,16 @@ __device__ __forceinline__ _Float16 half_sat(float x) {
     return _Float16(__builtin_fminf(__builtin_fmaxf(x, -65504.0f), 65504.0f));
 }
 
+// Status bits an expert's weight pair raises, as the address snapshot holds it: a null
+// address (status bit 0, a missing expert), or an address tagged in bit 0 (status bit 2, a
+// tiered slot address no live lease pins; real addresses are at least 4-byte aligned). The
+// expert's rows are written as zeros either way.
+__device__ __forceinline__ uint32_t weight_fault(const uint8_t* w0, const uint8_t* w1) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w0), b = reinterpret_cast<uintptr_t>(w1);
+    if (a == 0 || b == 0) return 1u;
+    return ((a | b) & 1u) ? 4u : 0u;
+}
+
 // Byte j (0..3) of a dword as an exact float (selected as v_cvt_f32_ubyte{j}).
 __device__ __forceinline__ float ubyte(uint32_t w, int j) { return float((w >> (8 * j)) & 0xffu); }
 

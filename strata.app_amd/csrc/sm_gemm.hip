@@ -184,8 +184,8 @@ __global__ __launch_bounds__(256) void routed_gemm_kernel(RoutedGemm g, uint32_t
     const uint64_t* addr = g.addresses + 3u * uint32_t(ex);
     const uint8_t* w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
     const uint8_t* w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
-    if (w0 == nullptr || w1 == nullptr) {
-        if (threadIdx.x == 0) atomicOr(g.status, 1u);
+    if (const uint32_t fault = weight_fault(w0, w1)) {
+        if (threadIdx.x == 0) atomicOr(g.status, fault);
         if (MODE == kGateUp) {
             zero_tile<MODE>(g, a0, a1, nt);
         } else {  // down rows live in route order

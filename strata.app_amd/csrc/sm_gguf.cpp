@@ -278,6 +278,17 @@ void sm_gguf_close(sm_gguf* g) {
 
 uint64_t sm_gguf_tensor_count(const sm_gguf* g) { return g ? g->tensors.size() : 0; }
 
+sm_status sm_internal_gguf_read(const sm_gguf* g, uint64_t offset, uint64_t bytes, void* dst) {
+    if (!g || !dst) return SM_E_ARGUMENT;
+    uint64_t got = 0;
+    while (got < bytes) {
+        const ssize_t rd = ::pread(g->fd, static_cast<uint8_t*>(dst) + got, bytes - got, off_t(offset + got));
+        if (rd <= 0) return SM_E_FILE;
+        got += uint64_t(rd);
+    }
+    return SM_OK;
+}
+
 sm_status sm_gguf_find(const sm_gguf* g, const char* name, sm_gguf_tensor* out) {
     if (!g || !name || !out) return SM_E_ARGUMENT;
     auto it = g->index.find(name);

@@ -52,9 +52,12 @@ struct GroupPrep {
     uint32_t* clear = nullptr;
     uint32_t clear_words = 0;
 };
+// resident (may be null: full residency): the selected layer's row of the I32 [layer][E]
+// residency table; a group's grp_res is resident[e] >= 0, n_miss counts the other groups and
+// skip = (n_miss == 0).
 hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
                            uint32_t* hist, Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst,
-                           const GroupPrep* prep, hipStream_t s);
+                           const GroupPrep* prep, const int32_t* resident, hipStream_t s);
 hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
                          const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
 

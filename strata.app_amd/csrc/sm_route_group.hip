@@ -342,7 +342,8 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
                                                                        uint32_t N, uint32_t n_tiles,
                                                                        Plan* __restrict__ plan,
                                                                        uint32_t* __restrict__ tiles,
-                                                                       uint32_t* __restrict__ arrive, GroupPrep prep) {
+                                                                       uint32_t* __restrict__ arrive, GroupPrep prep,
+                                                                       const int32_t* __restrict__ resident) {
     __shared__ uint32_t part[32][33];
     __shared__ uint32_t wave_tot[kScanThreads / 64];
     __shared__ uint32_t s_tstart[512], s_first[512], s_last;
@@ -400,6 +401,11 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
     const uint32_t grp = block_scan<kScanThreads>(count ? 1u : 0u, wave_tot, total_groups);
     const uint32_t ntile_e = (count + kExpertTile - 1) / kExpertTile;
     const uint32_t tstart = block_scan<kScanThreads>(ntile_e, wave_tot, total_tiles);
+    // Residency of the layer's experts (tiered mode): a used expert whose table entry is < 0
+    // is a miss the host resolves before the expert stages run.
+    const bool res = resident == nullptr || tid >= E || resident[tid] >= 0;
+    uint32_t total_miss;
+    (void)block_scan<kScanThreads>(count != 0u && !res ? 1u : 0u, wave_tot, total_miss);
     // Whole 6400-byte slot: every word defined (unused group slots -1 / 0, tail zero).
     uint32_t* words = reinterpret_cast<uint32_t*>(plan);
     for (uint32_t i = tid; i < kPlanSlotBytes / 4; i += kScanThreads) {
@@ -414,15 +420,15 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
     __syncthreads();
     if (count) {
         plan->grp_e[grp] = int32_t(tid);
-        plan->grp_res[grp] = 1;
+        plan->grp_res[grp] = res ? 1 : 0;
         plan->grp_start[grp] = int32_t(first);
     }
     if (tid < E) hist[uint64_t(n_tiles) * E + tid] = first;
     if (tid == 0) {
         plan->n_groups = total_groups;
         plan->n_entries = N;
-        plan->n_miss = 0;
-        plan->skip = 1;
+        plan->n_miss = total_miss;
+        plan->skip = total_miss == 0u ? 1u : 0u;
         plan->n_tiles = total_tiles;
         plan->bad = N - total_count;
         plan->grp_start[total_groups] = int32_t(total_count);
@@ -705,13 +711,14 @@ hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, 
 
 hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32_t E, uint32_t* hist,
                            Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst, const GroupPrep* prep,
+                           const int32_t* resident,
                            hipStream_t s) {
     const uint32_t N = rows * K;
     const uint32_t n_tiles = (N + kCountTile - 1) / kCountTile;
     uint32_t* arrive = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(plan) + kArriveBytes);
     group_count_kernel<<<n_tiles, 256, 0, s>>>(ids, N, E, hist, arrive);
     group_scan_plan_kernel<<<(E + 31) / 32, kScanThreads, 0, s>>>(hist, E, N, n_tiles, plan, tiles, arrive,
-                                                                  prep != nullptr ? *prep : GroupPrep{});
+                                                                  prep != nullptr ? *prep : GroupPrep{}, resident);
     group_scatter_kernel<<<n_tiles, 256, 0, s>>>(ids, N, K, E, n_tiles, hist, src, dst);
     return hipGetLastError();
 }

@@ -279,7 +279,7 @@ void encode_route_launch(sm_segment* seg, const sm_moe_shape& s, int divide, con
     });
 }
 
-struct GroupRes { uintptr_t ids, mixed, hist, plan, tiles, src, dst, gathered; };
+struct GroupRes { uintptr_t ids, mixed, hist, plan, tiles, src, dst, gathered, resident; };
 
 // The grouping histogram: the caller's view, or the fixed scratch (its view must then be null).
 bool hist_view(Check& c, const sm_view& v, uint64_t bytes, uintptr_t& out) {
@@ -294,6 +294,20 @@ bool hist_view(Check& c, const sm_view& v, uint64_t bytes, uintptr_t& out) {
     out = c.fixed->hist;
     return true;
 }
+// The residency table of tiered mode (prefill_moe_grouping.hpp:21-39): I32 [layer][E]; the
+// grouping reads row `layer` (pre-offset here). A null view is full residency.
+bool resident_view(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& b, GroupRes& r) {
+    r.resident = 0;
+    if (b.resident.buffer == 0) return true;
+    uint64_t need;
+    if (!mul_ok({uint64_t(b.layer) + 1, s.n_experts, 4}, need))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    uintptr_t p;
+    if (!c.view(b.resident, need, 4, "residency table", false, p)) return false;
+    r.resident = p + uint64_t(b.layer) * s.n_experts * 4;
+    return true;
+}
+
 bool check_grouping(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& b, GroupRes& r) {
     const uint64_t N = uint64_t(s.rows) * s.top_k;
     if (N > 0x7fffffffull) return c.fail(SM_E_SHAPE, c.prefix + " entry count exceeds kernel indexing");
@@ -309,7 +323,7 @@ bool check_grouping(Check& c, const sm_moe_shape& s, const sm_grouping_buffers& 
            c.view(b.tiles, tiles_b, 8, "tile list", true, r.tiles) &&
            c.view(b.source_rows, route_b, 4, "source rows", true, r.src) &&
            c.view(b.destination_rows, route_b, 4, "destination rows", true, r.dst) &&
-           c.view(b.gathered_rows, gath_b, 16, "gathered rows", true, r.gathered);
+           c.view(b.gathered_rows, gath_b, 16, "gathered rows", true, r.gathered) && resident_view(c, s, b, r);
 }
 
 // A full layer whose expert stages share one plan and tile list folds their checks into the
@@ -333,7 +347,8 @@ void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupR
         return sm::launch_grouping(reinterpret_cast<const int32_t*>(r.ids), rows, K, E,
                                    reinterpret_cast<uint32_t*>(r.hist), reinterpret_cast<sm::Plan*>(r.plan),
                                    reinterpret_cast<uint32_t*>(r.tiles), reinterpret_cast<int32_t*>(r.src),
-                                   reinterpret_cast<int32_t*>(r.dst), fused ? &prep : nullptr, st);
+                                   reinterpret_cast<int32_t*>(r.dst), fused ? &prep : nullptr,
+                                   reinterpret_cast<const int32_t*>(r.resident), st);
     });
     if (!fused) {
         add_step(seg, "gather", [=](hipStream_t st) {
@@ -384,6 +399,15 @@ bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, 
         if (!c.view(v, v.length, 1, "weight storage", false, p)) return false;
         storage.push_back({p, v.length, "weight storage", false, c.stage});
     }
+    // Tiered mode: the expert store's slot arena is storage too, but a slot address counts only
+    // while the lease set pins it for this layer (prefill_moe_expert_dispatch.mm:425-440).
+    Range arena{};
+    if (w.slot_arena.buffer != 0) {
+        uintptr_t p;
+        if (!c.view(w.slot_arena, w.slot_arena.length, 1, "slot arena", false, p)) return false;
+        arena = {p, w.slot_arena.length, "slot arena", false, c.stage};
+        storage.push_back(arena);
+    }
     const uint64_t* row = w.addresses + uint64_t(w.layer) * E * 3;  // the selected layer's [E][3]
     r.table.assign(row, row + E * 3);
     const uint64_t align = weight_align(fmt);
@@ -401,6 +425,11 @@ bool check_weights(Check& c, const sm_moe_shape& s, const sm_expert_weights& w, 
                               (unsigned long long)e, role == 0 ? "gate" : (role == 1 ? "up" : "down"));
                 return c.fail(SM_E_ADDRESS, c.prefix + msg);
             }
+            // An unpinned slot address is tagged in bit 0: the kernels then report status
+            // bit 2 for the expert (if it is active) and zero its rows instead of reading it.
+            if (arena.bytes != 0 && a >= arena.ptr && a - arena.ptr < arena.bytes &&
+                !(w.leases != nullptr && sm_lease_set_pins(w.leases, w.layer, a, expert_bytes)))
+                r.table[e * 3 + role] |= 1u;
         }
     }
     return true;
@@ -1030,7 +1059,7 @@ bool check_route_gather(Check& c, const sm_moe_shape& s, const sm_route_gather_b
     rr.logits = ro.logits;
     // Grouping reads the IDs the route step writes; validate its other views.
     sm_grouping_buffers gb{b.route_ids, b.mixed_h, b.histogram, b.plan, b.tiles, b.source_rows,
-                           b.destination_rows, b.gathered_rows};
+                           b.destination_rows, b.gathered_rows, b.resident, b.layer};
     const size_t n_in = c.inputs.size();
     if (!check_grouping(c, s, gb, gr)) return false;
     // Drop the duplicate input entries (route IDs and mixed activation are produced or

@@ -98,7 +98,8 @@ __device__ __forceinline__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32
 
 // Item `item` (tile k = item / n_chunks of the enumeration, column chunk item % n_chunks):
 // its rows, column tiles and weights. Returns false when the item is done already: an
-// expert without weights has zeroed its rows and set status bit 0. Uniform per workgroup.
+// expert without usable weights has zeroed its rows and set status bit 0 (missing) or 2
+// (unleased tiered slot). Uniform per workgroup.
 template <int MODE>
 __device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item, uint32_t n_ntiles,
                             uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t) {
@@ -119,8 +120,8 @@ __device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_
     const uint64_t* addr = g.addresses + 3u * ex;
     t.w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
     t.w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
-    if (t.w0 == nullptr || t.w1 == nullptr) {
-        if (threadIdx.x == 0) atomicOr(g.status, 1u);
+    if (const uint32_t fault = weight_fault(t.w0, t.w1)) {
+        if (threadIdx.x == 0) atomicOr(g.status, fault);
         zero_cols<MODE>(g, t.a0, t.a1, t.nt_begin * out_per_nt, t.nt_end * out_per_nt, MODE == kDown);
         return false;
     }

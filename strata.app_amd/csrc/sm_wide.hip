@@ -339,9 +339,10 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
             w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
             w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
         }
-        if (!DENSE && (w0 == nullptr || w1 == nullptr)) {
+        const uint32_t fault = DENSE ? 0u : weight_fault(w0, w1);
+        if (fault != 0u) {
             __syncthreads();
-            if (tid == 0) atomicOr(g.status, 1u);
+            if (tid == 0) atomicOr(g.status, fault);
             zero_item<MODE>(g, u, ct, s_dst);
             continue;
         }

@@ -46,7 +46,9 @@ EXPORTS = (
     "sm_build_chunk_schedule", "sm_chunk_count", "sm_chunk_range_at", "sm_encode_prefill_moe_chunks",
     "sm_submit_prefill_moe_chunks", "sm_submit_full_layer_fixed_scratch",
     "sm_gguf_open", "sm_gguf_close", "sm_gguf_tensor_count", "sm_gguf_find", "sm_gguf_expert_layout",
-    "sm_gguf_load_experts",
+    "sm_gguf_load_experts", "sm_expert_slot_bytes", "sm_expert_store_create", "sm_expert_store_destroy",
+    "sm_lease_set_create", "sm_lease_set_destroy", "sm_lease_set_retire_layer", "sm_lease_set_pins",
+    "sm_expert_store_resolve_layer",
     "sm_synth_normal_f32", "sm_synth_normal_f16", "sm_synth_normal_bf16", "sm_quantize",
     "sm_synth_quantized",
 )
@@ -71,19 +73,21 @@ class RouteBuffers(C.Structure):
 class GroupingBuffers(C.Structure):
     _fields_ = [("ids", View), ("mixed_h", View), ("histogram", View), ("plan", View),
                 ("tiles", View), ("source_rows", View), ("destination_rows", View),
-                ("gathered_rows", View)]
+                ("gathered_rows", View), ("resident", View), ("layer", C.c_uint32)]
 
 
 class RouteGatherBuffers(C.Structure):
     _fields_ = [("mixed_h", View), ("router_weights", View), ("logits", View),
                 ("route_ids", View), ("route_weights", View), ("histogram", View),
                 ("plan", View), ("tiles", View), ("source_rows", View),
-                ("destination_rows", View), ("gathered_rows", View), ("router_bias", View)]
+                ("destination_rows", View), ("gathered_rows", View), ("router_bias", View),
+                ("resident", View), ("layer", C.c_uint32)]
 
 
 class ExpertWeights(C.Structure):
     _fields_ = [("addresses", C.POINTER(C.c_uint64)), ("n_layers", C.c_uint32), ("layer", C.c_uint32),
-                ("address_snapshot", View), ("storage", C.POINTER(View)), ("n_storage", C.c_uint32)]
+                ("address_snapshot", View), ("storage", C.POINTER(View)), ("n_storage", C.c_uint32),
+                ("slot_arena", View), ("leases", C.c_void_p)]
 
 
 class GateUpBuffers(C.Structure):
@@ -133,6 +137,10 @@ class ExpertLayout(C.Structure):
     _fields_ = [("n_layers", C.c_uint32), ("n_experts", C.c_uint32), ("hidden", C.c_uint32), ("expert_ff", C.c_uint32),
                 ("gate_up", C.c_int), ("down", C.c_int), ("total_bytes", C.c_uint64),
                 ("offsets", (C.c_uint64 * 3) * GGUF_MAX_LAYERS)]
+
+
+class StoreStats(C.Structure):
+    _fields_ = [("hits", C.c_uint64), ("lookups", C.c_uint64), ("file_reads", C.c_uint64), ("file_bytes", C.c_uint64)]
 
 
 class ChunkSchedule(C.Structure):
@@ -202,6 +210,16 @@ def library() -> C.CDLL:
         "sm_gguf_expert_layout": (I, [P, U32, C.POINTER(ExpertLayout), C.c_char_p, C.c_size_t]),
         "sm_gguf_load_experts": (I, [P, P, P, C.POINTER(ExpertLayout), View, C.POINTER(C.c_uint64), U64, C.c_char_p,
                                      C.c_size_t]),
+        "sm_expert_slot_bytes": (U64, [C.POINTER(ExpertLayout)]),
+        "sm_expert_store_create": (I, [P, P, C.POINTER(ExpertLayout), View, U32, C.POINTER(P), C.c_char_p,
+                                       C.c_size_t]),
+        "sm_expert_store_destroy": (None, [P]),
+        "sm_lease_set_create": (I, [P, C.POINTER(P)]),
+        "sm_lease_set_destroy": (None, [P]),
+        "sm_lease_set_retire_layer": (None, [P, U32]),
+        "sm_lease_set_pins": (I, [P, U32, U64, U64]),
+        "sm_expert_store_resolve_layer": (I, [P, P, U32, View, P, C.POINTER(C.c_uint64), U64, C.POINTER(StoreStats),
+                                              C.c_char_p, C.c_size_t]),
         "sm_build_chunk_schedule": (I, [U32, U64, U32, C.POINTER(ChunkSchedule), C.c_char_p, C.c_size_t]),
         "sm_chunk_count": (U64, [C.POINTER(ChunkSchedule)]),
         "sm_chunk_range_at": (I, [C.POINTER(ChunkSchedule), U64, C.POINTER(ChunkRange)]),
@@ -325,15 +343,69 @@ class Context:
 
 class ExpertTable:
     """Host copy of the [layer][E][3] (gate, up, down) expert address table plus its storage;
-    `layer` selects the row the stage reads (the reference's `layer` argument)."""
+    `layer` selects the row the stage reads (the reference's `layer` argument). Tiered mode adds
+    the expert store's slot arena and the lease set that must pin its slot addresses."""
 
     def __init__(self, addresses: Sequence[int], snapshot: View, storage: Sequence[View], n_layers: int = 1,
-                 layer: int = 0):
+                 layer: int = 0, slot_arena: View = None, leases: "LeaseSet" = None):
         n = len(addresses)
         self._addr = (C.c_uint64 * n)(*addresses)
         self._storage = (View * max(1, len(storage)))(*storage)
+        self._leases = leases
         self.struct = ExpertWeights(C.cast(self._addr, C.POINTER(C.c_uint64)), n_layers, layer, snapshot,
-                                    C.cast(self._storage, C.POINTER(View)), len(storage))
+                                    C.cast(self._storage, C.POINTER(View)), len(storage),
+                                    slot_arena if slot_arena is not None else NULL_VIEW,
+                                    leases.handle if leases is not None else None)
+
+
+class ExpertStore:
+    """Tiered residency: a slot arena in two halves over the experts of a GGUF file (sm_expert_store_*)."""
+
+    def __init__(self, ctx: "Context", gguf: "GgufFile", layout: "ExpertLayout", arena: View, slots_per_half: int):
+        self.lib, self.ctx, self.gguf = library(), ctx, gguf
+        h = C.c_void_p()
+        err = C.create_string_buffer(512)
+        self.status = self.lib.sm_expert_store_create(ctx.handle, gguf.handle, C.byref(layout), arena, slots_per_half,
+                                                      C.byref(h), err, 512)
+        self.error = err.value.decode()
+        self.handle = h if self.status == 0 else None
+
+    def resolve_layer(self, stream, layer: int, plan: View, leases: "LeaseSet", table):
+        """resolve_layer_after_plan: (True, stats) or (False, message); `table` is a ctypes u64 array."""
+        stats = StoreStats()
+        err = C.create_string_buffer(512)
+        st = self.lib.sm_expert_store_resolve_layer(self.handle, C.c_void_p(stream), layer, plan, leases.handle,
+                                                    table, len(table), C.byref(stats), err, 512)
+        if st != 0:
+            return False, f"{STATUS_NAMES.get(st, st)}: {err.value.decode()}"
+        return True, dict(hits=stats.hits, lookups=stats.lookups, file_reads=stats.file_reads,
+                          file_bytes=stats.file_bytes)
+
+    def close(self):
+        if self.handle:
+            self.lib.sm_expert_store_destroy(self.handle)
+            self.handle = None
+
+
+class LeaseSet:
+    """Slot pins of one command sequence (sm_lease_set_*); destroy only after its GPU work completed."""
+
+    def __init__(self, store: ExpertStore):
+        self.lib = library()
+        h = C.c_void_p()
+        assert self.lib.sm_lease_set_create(store.handle, C.byref(h)) == 0
+        self.handle = h
+
+    def pins(self, layer: int, address: int, nbytes: int) -> bool:
+        return bool(self.lib.sm_lease_set_pins(self.handle, layer, address, nbytes))
+
+    def retire_layer(self, layer: int):
+        self.lib.sm_lease_set_retire_layer(self.handle, layer)
+
+    def close(self):
+        if self.handle:
+            self.lib.sm_lease_set_destroy(self.handle)
+            self.handle = None
 
 
 class GgufFile:
