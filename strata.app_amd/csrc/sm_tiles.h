@@ -178,23 +178,30 @@ struct Staged {
 
 // One 256-value slab of the wave's block. Only the first RB 16-row blocks of the tile hold
 // entries (the rest of a 64-row tile past its group's end would multiply padding), so the
-// others are skipped. after_s(s) runs after k-step s: the staged kernel issues part s of
-// the next step's copies there, so a wave never blocks on a long burst of memory
-// instructions while it could be multiplying.
+// others are skipped. The A fragments and decoded B fragments of k-step s + 1 are read and
+// decoded while the MFMAs of k-step s run (two register sets), so no MFMA waits on the LDS
+// read or the decode just before it. after_s(s) runs after k-step s: the staged kernel
+// issues part s of the next step's copies there, so a wave never blocks on a long burst of
+// memory instructions while it could be multiplying.
 template <class Frag, int NF, int RB, class After>
 __device__ __forceinline__ void slab_mma(const _Float16* buf, int n, int gq, const Frag (&c)[NF],
                                          float4v (&acc)[NF][4], After after_s) {
+    half8 a[2][RB], b[2][NF];
+    auto fetch = [&](int s, int z) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) a[z][rb] = *reinterpret_cast<const half8*>(buf + 8u * a_pos(16u * rb + n, 8u * gq + s));
+#pragma unroll
+        for (int f = 0; f < NF; ++f) b[z][f] = c[f].step(s);
+    };
+    fetch(0, 0);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        half8 b[NF];
+        const int z = s & 1;
+        if (s + 1 < 8) fetch(s + 1, z ^ 1);
 #pragma unroll
-        for (int f = 0; f < NF; ++f) b[f] = c[f].step(s);
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const half8 a = *reinterpret_cast<const half8*>(buf + 8u * a_pos(16u * rb + n, 8u * gq + s));
-#pragma unroll
-            for (int f = 0; f < NF; ++f) acc[f][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[f], acc[f][rb], 0, 0, 0);
-        }
+            for (int f = 0; f < NF; ++f) acc[f][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[z][rb], b[z][f], acc[f][rb], 0, 0, 0);
         after_s(s);
     }
 }
@@ -226,7 +233,9 @@ __device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint3
                 vecf v;
 #pragma unroll
                 for (int f = 0; f < NF; ++f) v[f] = good ? acc[f][rb][i] : 0.0f;
-                *reinterpret_cast<vecf*>(g.out_f + row * g.n_out + col0 + S::col(wave, n, 0)) = v;
+                // Write-once rows: non-temporal, so they do not evict the weight lines that the
+                // next step of this or another item still reads.
+                __builtin_nontemporal_store(v, reinterpret_cast<vecf*>(g.out_f + row * g.n_out + col0 + S::col(wave, n, 0)));
             }
         }
 #pragma unroll
@@ -394,10 +403,11 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
     wc.init(g, wave, lane);
     // Part p (0..7) of the copies of `step`: activation copy p (p < 4, streamed slabs only)
     // and weight items j with j % 8 == p.
-    auto issue_part = [&](uint32_t step, int p) {
-        const uint32_t nt = t.nt_begin + step / n_slabs, sb = step % n_slabs;
-        if (!RESIDENT && p < 4) issue_slab_part(asrc, sb * kSlab, sa[step & 1u], wave, p);
-        uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
+    // Part p (0..7) of the copies of step (nt, sb) into buffer `buf` (computed once per step by
+    // the caller: the division by n_slabs stays out of the k-step loop).
+    auto issue_part = [&](uint32_t nt, uint32_t sb, uint32_t buf, int p) {
+        if (!RESIDENT && p < 4) issue_slab_part(asrc, sb * kSlab, sa[buf], wave, p);
+        uint8_t* wb = sw[WBUF == 2 ? buf : 0u];
 #pragma unroll
         for (uint32_t j = uint32_t(p); j < WC::kPerWave; j += 8u) wc.issue(g, t, nt, sb, wb, wave, j);
     };
@@ -453,7 +463,7 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
         continue;
     }
 #pragma unroll
-    for (int p = 0; p < 8; ++p) issue_part(0, p);
+    for (int p = 0; p < 8; ++p) issue_part(t.nt_begin, 0u, 0u, p);
     // The step loop, specialised on the number of 16-row blocks holding entries.
     auto run = [&](auto rb_const) {
         constexpr int RB = decltype(rb_const)::value;
@@ -462,6 +472,7 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
         for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
+        uint32_t cur_nt = 0, cur_sb = 0;
         for (uint32_t step = 0; step < n_steps; ++step) {
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
             __syncthreads();                                       // ... from every wave
@@ -475,14 +486,17 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
             if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
 #pragma unroll
             for (int f = 0; f < NF; ++f) c[f].prepare();
-            const uint32_t sb = step % n_slabs;
+            // Column tile and slab of this step and the next (workgroup-uniform counters).
+            const uint32_t nt = t.nt_begin + cur_nt, sb = cur_sb;
+            const uint32_t nx_sb = sb + 1u == n_slabs ? 0u : sb + 1u;
+            const uint32_t nx_nt = sb + 1u == n_slabs ? nt + 1u : nt;
             slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [&](int p) {
-                if (more) issue_part(step + 1, p);
+                if (more) issue_part(nx_nt, nx_sb, (step + 1u) & 1u, p);
             });
-            if (sb == n_slabs - 1u) {  // column tile complete
-                const uint32_t nt = t.nt_begin + step / n_slabs;
+            if (sb == n_slabs - 1u)  // column tile complete
                 staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
-            }
+            cur_sb = nx_sb;
+            cur_nt = nx_nt - t.nt_begin;
         }
     };
     switch ((t.a1 - t.a0 + 15u) / 16u) {  // workgroup-uniform

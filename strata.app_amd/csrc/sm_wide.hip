@@ -488,8 +488,8 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
                         const bool good = DENSE || d < g.n_entries;
                         any_bad = any_bad || !good;
                         float* out = g.out_f + uint64_t(good ? d : a) * n_out + col0;
-                        out[0] = good ? acc[rb][0][i] : 0.0f;
-                        out[32] = good ? acc[rb][1][i] : 0.0f;
+                        __builtin_nontemporal_store(good ? acc[rb][0][i] : 0.0f, out);  // write-once rows
+                        __builtin_nontemporal_store(good ? acc[rb][1][i] : 0.0f, out + 32);
                     }
                 }
         };
