@@ -484,15 +484,20 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
             // A barrier waits for every outstanding load of the wave, so with one weight image
             // the next step's copies start only after the second barrier.
             if (WBUF == 1) __syncthreads();  // every wave holds its fragments: the image may be refilled
-#pragma unroll
-            for (int f = 0; f < NF; ++f) c[f].prepare();
             // Column tile and slab of this step and the next (workgroup-uniform counters).
             const uint32_t nt = t.nt_begin + cur_nt, sb = cur_sb;
             const uint32_t nx_sb = sb + 1u == n_slabs ? 0u : sb + 1u;
             const uint32_t nx_nt = sb + 1u == n_slabs ? nt + 1u : nt;
-            slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [&](int p) {
-                if (more) issue_part(nx_nt, nx_sb, (step + 1u) & 1u, p);
-            });
+            // Every copy of the next step is issued here, a whole step ahead of its wait (the
+            // buffers it fills were last read in the previous step, or, with one weight image,
+            // before the second barrier).
+            if (more) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) issue_part(nx_nt, nx_sb, (step + 1u) & 1u, p);
+            }
+#pragma unroll
+            for (int f = 0; f < NF; ++f) c[f].prepare();
+            slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [](int) {});
             if (sb == n_slabs - 1u)  // column tile complete
                 staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
             cur_sb = nx_sb;
