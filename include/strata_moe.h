@@ -289,6 +289,137 @@ sm_status sm_encode_dequant(sm_segment* seg, sm_format fmt, uint32_t n_out, uint
 sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape,
                                const sm_layer_formats* formats, const sm_layer_buffers* b);
 
+/* ---- decode-side MoE (the reference's Window MoE over T = 1..8 rows) -----------------------
+ * The step after prefill on the same layer (include/strata/metal/moe_dispatch.hpp:13-372,
+ * src/metal/kernels/safe/moe.metal:101-275, docs/mac/04-metal-kernels.md sections 5.8, 5.10):
+ * a first-appearance expert plan, Q8_1 activations, grouped mat-vecs that read each active
+ * expert's weights once per group, an F32 SwiGLU and the decode combine. The expert formats
+ * are this library's block formats (Q8_0, Q4_K, Q2_K) over the same [layer][E][3] address
+ * table as prefill. hidden is a multiple of 256 and expert_ff of 64 (K-quant down weights need
+ * expert_ff in whole 256-value super-blocks; the reference model's 2560 / 640 fit); rows * top_k <= 80.
+ * Status word (one per coordinator call, cleared on the GPU first): bit 0 an active expert's
+ * address is null, bit 1 the plan is unusable (an id outside [0, E), a malformed header or
+ * entry), bit 2 an active expert's tiered slot is not leased. Failing groups write zeros. */
+#define SM_DECODE_MAX_ROWS 8u
+#define SM_MOE_PLAN_BYTES 1620u       /* MoePlan, moe.metal:101-111 (TieredMoePlan, tiered.hpp:24-36) */
+#define SM_MOE_PLAN_MAX_ENTRIES 80u   /* T * k <= 8 * 10                                        */
+#define SM_Q8_1_BLOCK_BYTES 36u       /* Q81 {half d, half sum; int8 q[32]}, types.h:128-131     */
+
+/* MoePlanBuffers (moe_dispatch.hpp:19-24). The plan, residency and usage views start at layer 0
+ * and contain the selected layer: plan `plans + layer * 1620`, rows `layer * E` of the I32
+ * residency and F32 usage tables (tiered mode: usage += 1 per routed entry; null views = full
+ * mode, every group resident). */
+typedef struct sm_moe_plan_buffers {
+    sm_view ids;                /* I32 [T*k] route ids, token-major                         */
+    sm_view resident;           /* I32 [layer+1][E] or null                                 */
+    sm_view usage;              /* F32 [layer+1][E] or null                                 */
+    sm_view plans;              /* MoePlan [layer+1]                                        */
+    sm_view status;             /* U32 or null                                              */
+    uint32_t layer;
+} sm_moe_plan_buffers;
+
+/* MoeGroupedExpertBuffers (moe_dispatch.hpp:37-51): gate and up, F32, in grouped entry order. */
+typedef struct sm_moe_expert_buffers {
+    sm_expert_weights weights;  /* layer = the plan's layer                                 */
+    sm_view activations;        /* Q8_1 [T][d/32]                                           */
+    sm_view plans;              /* MoePlan table from layer 0                               */
+    sm_view gate;               /* F32 [T*k][I]                                             */
+    sm_view up;                 /* F32 [T*k][I]                                             */
+    sm_view status;             /* U32                                                      */
+} sm_moe_expert_buffers;
+
+/* MoeGroupedDownBuffers (moe_dispatch.hpp:54-63): parts F32 in route order. */
+typedef struct sm_moe_down_buffers {
+    sm_expert_weights weights;
+    sm_view activations;        /* Q8_1 [T*k][I/32], grouped entry order                   */
+    sm_view plans;
+    sm_view parts;              /* F32 [T*k][d], row t*k + rank                             */
+    sm_view status;
+} sm_moe_down_buffers;
+
+/* MoeSwiGLUBuffers (moe_dispatch.hpp:82-86): F32 silu(gate) * up. */
+typedef struct sm_moe_swiglu_buffers {
+    sm_view gate;
+    sm_view up;
+    sm_view output;
+} sm_moe_swiglu_buffers;
+
+/* MoeRoutedFFNBuffers (moe_dispatch.hpp:65-80): gate/up, SwiGLU, Q8_1, down in one segment. */
+typedef struct sm_moe_routed_ffn_buffers {
+    sm_expert_weights gate_up_weights;
+    sm_expert_weights down_weights;
+    sm_view input_activations;  /* Q8_1 [T][d/32]                                           */
+    sm_view plans;
+    sm_view gate;               /* F32 [T*k][I] scratch                                     */
+    sm_view up;
+    sm_view hidden;
+    sm_view down_activations;   /* Q8_1 [T*k][I/32] scratch                                 */
+    sm_view parts;              /* F32 [T*k][d]                                             */
+    sm_view status;
+} sm_moe_routed_ffn_buffers;
+
+/* MoeSharedFFNBuffers (moe_dispatch.hpp:101-135): the shared expert over T <= 8 rows, then the
+ * decode combine with the routed parts. This library's shared weights are F16/BF16 [Is][d]
+ * (down [d][Is]) read by dense mat-vecs; shared.hidden is F32 [T][Is] = silu(x.Wg) * (x.Wu). */
+typedef struct sm_moe_shared_ffn_buffers {
+    sm_shared_buffers shared;   /* hidden F32 [T][Is]; output F32 [T][d]; gate_logit F32 [T] */
+    sm_view routed_parts;       /* F32 [T*k][d], route order                                */
+    sm_view route_weights;      /* F32 [T,k]                                                */
+    sm_view output;             /* F32 [T,d]                                                */
+} sm_moe_shared_ffn_buffers;
+
+/* One decode layer: router GEMM, top-k in multiply mode (the Window's route, moe_dispatch.hpp:
+ * 161-168), plan (+ both address snapshots), Q8_1 of the input, the routed FFN, the shared
+ * expert (F16/BF16 mat-vecs on mixed_h, as sm_encode_moe_shared_ffn) and the decode combine. */
+typedef struct sm_decode_layer_buffers {
+    sm_view mixed_h;            /* F16 [T,d]                                                */
+    sm_view router_weights;     /* F32 [E,d]                                                */
+    sm_view router_bias;        /* F32 [E] or null                                          */
+    sm_view logits;             /* F32 [T,E]                                                */
+    sm_view route_ids;          /* I32 [T,k]                                                */
+    sm_view route_weights;      /* F32 [T,k]                                                */
+    sm_view resident;           /* tiered mode, as in sm_moe_plan_buffers (or null)         */
+    sm_view usage;
+    sm_view plans;
+    uint32_t layer;
+    sm_view input_activations;  /* Q8_1 [T][d/32] scratch                                   */
+    sm_moe_routed_ffn_buffers routed;  /* its input_activations and plans views are ignored  */
+    sm_shared_buffers shared;   /* shared_ff == 0: ignored; mixed_h must equal mixed_h; hidden F32 [T][Is] */
+    sm_view output;             /* F32 [T,d]                                                */
+} sm_decode_layer_buffers;
+
+/* encode_moe_plan — moe_dispatch.hpp:184-188. */
+sm_status sm_encode_moe_plan(sm_segment* seg, const sm_moe_shape* shape, const sm_moe_plan_buffers* b);
+/* strata_q_q8_1 — 04-metal-kernels.md section 5.8 (quantize_q8_1.metal): rows x n values
+ * (n a multiple of 32; F16 input, or F32 when f32_input != 0) to Q8_1 blocks. */
+sm_status sm_encode_quantize_q8_1(sm_segment* seg, uint32_t rows, uint32_t n, int f32_input, sm_view input,
+                                  sm_view output);
+/* encode_moe_experts — moe_dispatch.hpp:203-208. */
+sm_status sm_encode_moe_experts(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                                const sm_moe_expert_buffers* b);
+/* encode_moe_down — moe_dispatch.hpp:223-228. */
+sm_status sm_encode_moe_down(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                             const sm_moe_down_buffers* b);
+/* encode_moe_swiglu — moe_dispatch.hpp:264-267: rows x width F32 values. */
+sm_status sm_encode_moe_swiglu(sm_segment* seg, uint32_t rows, uint32_t width, const sm_moe_swiglu_buffers* b);
+/* encode_moe_routed_ffn — moe_dispatch.hpp:244-250. */
+sm_status sm_encode_moe_routed_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format gate_up_fmt,
+                                   sm_format down_fmt, const sm_moe_routed_ffn_buffers* b);
+/* encode_moe_combine — moe_dispatch.hpp:277-280 (the decode combine: the first rank a product,
+ * the others fma, the gated shared output added last; moe.metal:253-274). */
+sm_status sm_encode_moe_combine(sm_segment* seg, const sm_moe_shape* shape, const sm_combine_buffers* b);
+/* encode_moe_shared_ffn — moe_dispatch.hpp:287-308: shared gate/up + F32 SwiGLU, down, the
+ * sigmoid gate logit, then the decode combine (4 launches). */
+sm_status sm_encode_moe_shared_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                                   const sm_moe_shared_ffn_buffers* b);
+/* The Window MoE FFN of one layer (moe_dispatch.hpp:339-372's composition, with the route and
+ * plan in front): see sm_decode_layer_buffers. */
+sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* formats,
+                                     const sm_decode_layer_buffers* b);
+sm_status sm_submit_moe_decode_layer(sm_context* ctx, void* hip_stream, const sm_moe_shape* shape,
+                                     const sm_layer_formats* formats, const sm_decode_layer_buffers* b, char* err,
+                                     size_t err_cap);
+
 /* ---- chunk driver (the reference's Prefill::run chunk loop) ------------------------------ */
 /* PrefillChunkSchedule (include/strata/metal/prefill.hpp:47-72): a prompt of token_count
  * tokens starting at cell pos0, split into contiguous, unpadded ranges of at most chunk_rows. */

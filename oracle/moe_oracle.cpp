@@ -523,3 +523,243 @@ float silu_f(float x) { return silu(x); }
 uint16_t half_sat_f(float x) { return half_sat(x); }
 float f16_f(uint16_t h) { return f16_to_f32(h); }
 }  // namespace oracle_internal
+
+// =========================================================================================
+// Decode-side MoE (the reference's Window MoE over T <= 8 rows).
+// =========================================================================================
+namespace {
+
+struct DecodePlanLayout {  // MoePlan, moe.metal:101-111 (1620 bytes)
+    uint32_t n_groups, n_entries, n_miss, skip;
+    int32_t grp_e[80], grp_res[80], grp_start[81], ent_tok[80], ent_dst[80];
+};
+static_assert(sizeof(DecodePlanLayout) == 1620, "MoePlan host layout");
+
+constexpr uint32_t kQ81 = 36;  // half d, half sum, int8 q[32] (types.h:128-131)
+
+// Sum of 32 lanes as the butterfly leaves it in lane 0: after each xor offset o (16 .. 1) lane
+// l holds v[l] + v[l ^ o] of the previous level.
+float butterfly32(const float* x) {
+    float v[32];
+    std::memcpy(v, x, sizeof v);
+    for (uint32_t o = 16; o; o >>= 1) {
+        float nv[32];
+        for (uint32_t l = 0; l < 32; ++l) nv[l] = v[l] + v[l ^ o];
+        std::memcpy(v, nv, sizeof v);
+    }
+    return v[0];
+}
+
+// One 32-value weight block b of a row as integer codes and its scales: value i of the block
+// is d*sc[i/16]*q[i] - dmin*mn[i/16] (Q8_0: sc = 1, dmin = 0).
+struct WBlock {
+    int q[32];
+    double d, dmin;
+    int sc[2], mn[2];
+};
+
+void weight_block(int fmt, const uint8_t* row, uint32_t b, WBlock& w) {
+    switch (fmt) {
+        case OR_FMT_Q8_0: {  // dequant.hpp:81-86
+            const uint8_t* p = row + 34u * b;
+            w.d = f16_to_f32(rd16(p));
+            w.dmin = 0.0;
+            w.sc[0] = w.sc[1] = 1;
+            w.mn[0] = w.mn[1] = 0;
+            for (int i = 0; i < 32; ++i) w.q[i] = int8_t(p[2 + i]);
+            break;
+        }
+        case OR_FMT_Q4_K: {  // dequant.hpp:157-190: sub-block j = values 32j .. 32j+31
+            const uint8_t* p = row + 144u * (b / 8);
+            const uint32_t j = b % 8;
+            uint8_t sc, m;
+            scale_min_k4(int(j), p + 4, sc, m);
+            w.d = f16_to_f32(rd16(p));
+            w.dmin = f16_to_f32(rd16(p + 2));
+            w.sc[0] = w.sc[1] = sc;
+            w.mn[0] = w.mn[1] = m;
+            for (int i = 0; i < 32; ++i) {
+                const uint8_t byte = p[16 + 32 * (j / 2) + i];
+                w.q[i] = (j & 1) ? byte >> 4 : byte & 0x0F;
+            }
+            break;
+        }
+        case OR_FMT_Q2_K: {  // ggml-common.h:298-309 layout, dequantize_row_q2_K values
+            const uint8_t* p = row + 84u * (b / 8);
+            const uint32_t e0 = 32u * (b % 8), n = e0 / 128, j = (e0 % 128) / 32;
+            w.d = f16_to_f32(rd16(p + 80));
+            w.dmin = f16_to_f32(rd16(p + 82));
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t s = p[8 * n + 2 * j + h];
+                w.sc[h] = s & 0xF;
+                w.mn[h] = s >> 4;
+            }
+            for (int i = 0; i < 32; ++i) w.q[i] = (p[16 + 32 * n + i] >> (2 * j)) & 3;
+            break;
+        }
+        default:
+            std::memset(&w, 0, sizeof w);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// The decode expert plan (moe.metal:123-210): groups in order of each expert's first
+// appearance among the n = rows*top_k route entries; a group's entries are its expert's
+// entries in index order, packed after the previous groups'. Built here by walking each first
+// appearance's members.
+int or_moe_plan(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                const int32_t* resident, float* usage, uint8_t* plan_out) {
+    const uint32_t n = rows * top_k;
+    if (rows == 0 || top_k == 0 || n > 80 || n_experts == 0) return -1;
+    DecodePlanLayout p;
+    std::memset(&p, 0, sizeof p);
+    bool bad = false;
+    for (uint32_t i = 0; i < n; ++i) bad = bad || ids[i] < 0 || uint32_t(ids[i]) >= n_experts;
+    if (bad) {  // an empty plan (this build's status bit 1; the reference does not check)
+        p.skip = 1;
+        std::memcpy(plan_out, &p, sizeof p);
+        return 1;
+    }
+    uint32_t entry = 0;
+    for (uint32_t j = 0; j < n; ++j) {
+        bool seen = false;
+        for (uint32_t i = 0; i < j && !seen; ++i) seen = ids[i] == ids[j];
+        if (seen) continue;
+        const uint32_t g = p.n_groups++;
+        const bool res = resident == nullptr || resident[ids[j]] >= 0;
+        p.grp_e[g] = ids[j];
+        p.grp_start[g] = int32_t(entry);
+        p.grp_res[g] = res ? 1 : 0;
+        p.n_miss += res ? 0 : 1;
+        for (uint32_t i = j; i < n; ++i)
+            if (ids[i] == ids[j]) {
+                p.ent_dst[entry] = int32_t(i);
+                p.ent_tok[entry] = int32_t(i / top_k);
+                ++entry;
+            }
+    }
+    p.grp_start[p.n_groups] = int32_t(entry);
+    p.n_entries = n;
+    p.skip = p.n_miss == 0 ? 1 : 0;
+    if (usage != nullptr)
+        for (uint32_t i = 0; i < n; ++i) usage[ids[i]] += 1.0f;
+    std::memcpy(plan_out, &p, sizeof p);
+    return 0;
+}
+
+// The precise Q8_1 quantizer (quantize_q8_1.metal; tests/metal/oracles/q8_1.cpp:56-124): per
+// 32-value block, amax = max |x|, d = amax / 127 in F32 and q = round(x / d), half away from
+// zero, clamped to +-127 when d is subnormal. Where d rounds to zero although amax is not
+// zero, q = round(127 x / amax) of the exact ratio (half away from zero, at most 127). The
+// block stores f16(d) and f16 of the values' butterfly sum.
+// The F32 quotient is formed in double and rounded once to float: for a quotient of two
+// floats that equals the correctly rounded F32 quotient (53 >= 2*24 + 2 bits), so the result
+// does not depend on the host's denormal mode.
+int or_quantize_q8_1(const float* x, uint32_t rows, uint32_t n, uint8_t* out) {
+    if (rows == 0 || n == 0 || n % 32 != 0) return -1;
+    const uint32_t nb = n / 32;
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t b = 0; b < nb; ++b) {
+            const float* v = x + uint64_t(r) * n + 32u * b;
+            uint8_t* blk = out + (uint64_t(r) * nb + b) * kQ81;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                if (!std::isfinite(v[i])) return -2;
+                amax = std::fmax(amax, std::fabs(v[i]));
+            }
+            const float d = float(double(amax) / 127.0);
+            const uint32_t db = fbits(d);
+            const uint16_t hd = f32_to_f16(d), hs = f32_to_f16(butterfly32(v));
+            blk[0] = uint8_t(hd);
+            blk[1] = uint8_t(hd >> 8);
+            blk[2] = uint8_t(hs);
+            blk[3] = uint8_t(hs >> 8);
+            for (int i = 0; i < 32; ++i) {
+                double q = 0.0;
+                if (amax != 0.0f) {
+                    if (db == 0u) {
+                        q = std::min(std::round(127.0 * std::fabs(double(v[i])) / double(amax)), 127.0);
+                        if (std::signbit(v[i])) q = -q;
+                    } else {
+                        q = std::round(double(float(double(v[i]) / double(d))));
+                        if ((db & 0x7f800000u) == 0u) q = std::min(std::max(q, -127.0), 127.0);
+                    }
+                }
+                blk[4 + i] = uint8_t(int8_t(int(q)));
+            }
+        }
+    return 0;
+}
+
+// Grouped decode mat-vec value in FP64: out[c][r] = sum over the 32-value blocks of row r of
+// dx * (d * sum_h sc_h * sum(qw * qx) - dmin * sum_h mn_h * sum(qx)), the exact product of
+// the dequantized weights (d*sc*q - dmin*mn) with the Q8_1 codes times dx
+// (q8_0_mv.cpp:21-33, q4_k_mv.cpp:26-70 for the split). mag[c][r] (optional) sums the two
+// terms' magnitudes per block: the scale of the F32 rounding a GPU accumulation may add.
+int or_q81_matvec(int fmt, const uint8_t* w, uint32_t n_out, uint32_t k, const uint8_t* act,
+                  uint32_t nc, double* out, double* mag) {
+    const uint64_t rb = row_bytes(fmt, k);
+    if (rb == 0 || k % 32 != 0 || n_out == 0 || nc == 0 || fmt == OR_FMT_F16 || fmt == OR_FMT_BF16) return -1;
+    const uint32_t nb = k / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < int64_t(n_out); ++r) {
+        const uint8_t* row = w + uint64_t(r) * rb;
+        std::vector<double> acc(nc, 0.0), am(nc, 0.0);
+        WBlock wb;
+        for (uint32_t b = 0; b < nb; ++b) {
+            weight_block(fmt, row, b, wb);
+            for (uint32_t c = 0; c < nc; ++c) {
+                const uint8_t* ab = act + (uint64_t(c) * nb + b) * kQ81;
+                const double dx = f16_to_f32(rd16(ab));
+                int64_t s[2] = {0, 0}, t[2] = {0, 0};
+                for (int i = 0; i < 32; ++i) {
+                    const int qx = int8_t(ab[4 + i]);
+                    s[i / 16] += int64_t(wb.q[i]) * qx;
+                    t[i / 16] += qx;
+                }
+                const double sd = wb.d * double(wb.sc[0] * s[0] + wb.sc[1] * s[1]);
+                const double sm = wb.dmin * double(wb.mn[0] * t[0] + wb.mn[1] * t[1]);
+                acc[c] += dx * (sd - sm);
+                am[c] += std::fabs(dx) * (std::fabs(sd) + std::fabs(sm));
+            }
+        }
+        for (uint32_t c = 0; c < nc; ++c) {
+            out[uint64_t(c) * n_out + r] = acc[c];
+            if (mag) mag[uint64_t(c) * n_out + r] = am[c];
+        }
+    }
+    return 0;
+}
+
+// The decode SwiGLU, moe.metal:213-221: silu(g) * u in F32.
+int or_swiglu_f32(const float* gate, const float* up, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = silu(gate[i]) * up[i];
+    return 0;
+}
+
+// The decode combine, moe.metal:253-274: the first rank's product, fma over the other ranks
+// in order, then the gated shared term added as a separately rounded product.
+int or_combine_decode(const float* parts, const float* w, const float* shared, const float* gl,
+                      uint32_t rows, uint32_t K, uint32_t d, float* out) {
+    if (rows == 0 || K == 0 || d == 0) return -1;
+    for (uint32_t t = 0; t < rows; ++t) {
+        const float* p = parts + uint64_t(t) * K * d;
+        const float* wt = w + uint64_t(t) * K;
+        const float gs = shared ? sigmoid(gl[t]) : 0.0f;
+        for (uint32_t c = 0; c < d; ++c) {
+            float s = p[c] * wt[0];
+            for (uint32_t r = 1; r < K; ++r) s = std::fma(p[uint64_t(r) * d + c], wt[r], s);
+            if (shared) {
+                const float term = shared[uint64_t(t) * d + c] * gs;
+                s = s + term;
+            }
+            out[uint64_t(t) * d + c] = s;
+        }
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -18,6 +18,11 @@
  *                           src/metal/kernels/common/math.h:6-40
  *   combine ............... src/metal/kernels/safe/prefill_moe.metal:1201-1222,
  *                           tests/metal/oracles/moe_combine.cpp:8-57
+ *   decode plan ........... src/metal/kernels/safe/moe.metal:101-210
+ *   Q8_1 quantizer ........ src/metal/kernels/safe/quantize_q8_1.metal,
+ *                           tests/metal/oracles/q8_1.cpp:56-124
+ *   Q8_1 mat-vecs ......... tests/metal/oracles/q8_0_mv.cpp:21-106, q4_k_mv.cpp:26-154
+ *   decode SwiGLU/combine . src/metal/kernels/safe/moe.metal:213-274
  *   dequant Q8_0 / Q4_K ... include/strata/artifact/dequant.hpp:80-86,157-190,
  *                           src/metal/kernels/prefill_dequant.metal:12-56,341-361
  *   dequant Q2_K .......... third_party/ggml/ggml-common.h:298-309 (layout only; the value
@@ -35,6 +40,14 @@
  *   or_combine / or_swiglu ... the reference's moe_combine.cpp / moe_swiglu.cpp in oracle/_ref,
  *                   and a double-precision formula.
  *   GEMM refs ..... FP64 sums of exact products; checked against numpy float64 matmul.
+ *   or_moe_plan ... brute-force plan invariants (each entry once, contiguous groups in
+ *                   first-appearance order, ascending members) and hand-worked plans.
+ *   or_quantize_q8_1 ... the reference's q8_1.cpp in oracle/_ref, bit for bit, over random,
+ *                   subnormal, zero and huge blocks.
+ *   or_q81_matvec . the reference's q8_0_mv.cpp / q4_k_mv.cpp in oracle/_ref (F32 twins, within
+ *                   their rounding) and, exactly, FP64 dots of or_dequant values on weights
+ *                   whose dequantized values are exact in F16 (Q8_0, Q4_K, Q2_K).
+ *   or_swiglu_f32 / or_combine_decode ... moe_swiglu.cpp / moe_combine.cpp in oracle/_ref.
  *
  * All arrays are host memory. F16 values are passed as their uint16 bit patterns.
  * Functions return 0 on success and a negative value on a shape error.
@@ -117,6 +130,24 @@ int or_swiglu(const float* gate, const float* up, uint64_t n, uint16_t* out);
  * shared/gl may be NULL (no shared expert): out = ordered sum. */
 int or_combine(const float* parts, const float* weights, const float* shared, const float* gl,
                uint32_t rows, uint32_t top_k, uint32_t d, float* out);
+
+/* ---- decode-side MoE (the Window MoE, T <= 8 rows; moe.metal:101-275) ----
+ * or_moe_plan: the 1620-byte MoePlan of n = rows*top_k <= 80 entries. resident (per expert,
+ *   >= 0 means resident) and usage (+1 per entry) may be NULL. Returns 1 and an empty plan
+ *   (skip = 1, everything else zero) when an id is outside [0, n_experts).
+ * or_quantize_q8_1: rows x n F32 values (n % 32 == 0, finite) to 36-byte Q8_1 blocks.
+ * or_q81_matvec: out/mag [nc][n_out] in FP64 for n_out rows of k values in fmt (Q8_0, Q4_K,
+ *   Q2_K) against nc Q8_1 activation rows of k values; mag may be NULL.
+ * or_swiglu_f32: out = silu(g) * u in F32. or_combine_decode: the decode combine; shared/gl
+ *   may be NULL. */
+int or_moe_plan(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
+                const int32_t* resident, float* usage, uint8_t* plan_out);
+int or_quantize_q8_1(const float* x, uint32_t rows, uint32_t n, uint8_t* out);
+int or_q81_matvec(int fmt, const uint8_t* w, uint32_t n_out, uint32_t k, const uint8_t* act,
+                  uint32_t nc, double* out, double* mag);
+int or_swiglu_f32(const float* gate, const float* up, uint64_t n, float* out);
+int or_combine_decode(const float* parts, const float* w, const float* shared, const float* gl,
+                      uint32_t rows, uint32_t top_k, uint32_t d, float* out);
 
 /* ---- timed CPU baseline of the whole layer (F32 accumulation, OpenMP) ----
  * Stages, in order of stage_us[]: 0 router GEMM, 1 top-k, 2 grouping+gather, 3 shared FFN,

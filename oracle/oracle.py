@@ -64,6 +64,11 @@ def _bind(L: C.CDLL) -> C.CDLL:
         "or_shared_ref": (I, [I, P, U32, U32, P, P, P, P, P, U32, P, P, P]),
         "or_swiglu": (I, [P, P, U64, P]),
         "or_combine": (I, [P, P, P, P, U32, U32, U32, P]),
+        "or_moe_plan": (I, [P, U32, U32, U32, P, P, P]),
+        "or_quantize_q8_1": (I, [P, U32, U32, P]),
+        "or_q81_matvec": (I, [I, P, U32, U32, P, U32, P, P]),
+        "or_swiglu_f32": (I, [P, P, U64, P]),
+        "or_combine_decode": (I, [P, P, P, P, U32, U32, U32, P]),
         "or_cpu_layer": (I, [U32, U32, U32, U32, U32, U32, I, I, I, P, P, P, P, U64, P, U64,
                              P, P, P, P, I, P, P]),
     }
@@ -81,6 +86,9 @@ def ref() -> C.CDLL | None:
         R.ref_route.argtypes = [P, C.c_uint32, C.c_uint32, C.c_int, P, P]
         R.ref_combine.argtypes = [P, P, P, P, C.c_uint32, P]
         R.ref_swiglu.argtypes = [P, P, C.c_uint64, P]
+        R.ref_q8_1.argtypes = [P, C.c_uint32, C.c_uint32, P]
+        R.ref_q80_mv.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P]
+        R.ref_q4k_mv.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P]
         _ref = R
     return _ref
 
@@ -194,6 +202,62 @@ def combine(parts, weights, shared, gl, rows, top_k, d):
                             _p(None if shared is None else np.ascontiguousarray(shared, np.float32)),
                             _p(None if gl is None else np.ascontiguousarray(gl, np.float32)),
                             rows, top_k, d, _p(out)) == 0
+    return out
+
+
+# ---- decode-side MoE ----------------------------------------------------------------------
+PLAN_DTYPE = np.dtype([("n_groups", "<u4"), ("n_entries", "<u4"), ("n_miss", "<u4"), ("skip", "<u4"),
+                       ("grp_e", "<i4", 80), ("grp_res", "<i4", 80), ("grp_start", "<i4", 81),
+                       ("ent_tok", "<i4", 80), ("ent_dst", "<i4", 80)])
+assert PLAN_DTYPE.itemsize == 1620
+
+
+def moe_plan(ids: np.ndarray, n_experts: int, resident: np.ndarray | None = None,
+             usage: np.ndarray | None = None):
+    """MoePlan bytes (1620) and the return code (0, or 1 for an out-of-range id)."""
+    rows, top_k = ids.shape
+    ids = np.ascontiguousarray(ids, np.int32)
+    res = None if resident is None else np.ascontiguousarray(resident, np.int32)
+    plan = np.zeros(1620, np.uint8)
+    rc = lib().or_moe_plan(_p(ids), rows, top_k, n_experts, _p(res), _p(usage), _p(plan))
+    assert rc in (0, 1)
+    return plan, rc
+
+
+def quantize_q8_1(x: np.ndarray) -> np.ndarray:
+    """[rows, n] F32 values (F16 inputs are widened first) -> [rows, n/32 * 36] Q8_1 bytes."""
+    x = np.ascontiguousarray(np.asarray(x).astype(np.float32))
+    rows, n = x.shape
+    out = np.empty((rows, n // 32 * 36), np.uint8)
+    assert lib().or_quantize_q8_1(_p(x), rows, n, _p(out)) == 0
+    return out
+
+
+def q81_matvec(fmt: int, w: np.ndarray, n_out: int, k: int, act: np.ndarray):
+    """FP64 [nc, n_out] values and magnitudes of n_out weight rows against nc Q8_1 rows."""
+    w = np.ascontiguousarray(w, np.uint8)
+    act = np.ascontiguousarray(act, np.uint8)
+    nc = act.size // (k // 32 * 36)
+    out = np.empty((nc, n_out), np.float64)
+    mag = np.empty((nc, n_out), np.float64)
+    assert lib().or_q81_matvec(fmt, _p(w), n_out, k, _p(act), nc, _p(out), _p(mag)) == 0
+    return out, mag
+
+
+def swiglu_f32(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, np.float32)
+    up = np.ascontiguousarray(up, np.float32)
+    out = np.empty(gate.shape, np.float32)
+    assert lib().or_swiglu_f32(_p(gate), _p(up), gate.size, _p(out)) == 0
+    return out
+
+
+def combine_decode(parts, weights, shared, gl, rows, top_k, d):
+    out = np.empty((rows, d), np.float32)
+    assert lib().or_combine_decode(
+        _p(np.ascontiguousarray(parts, np.float32)), _p(np.ascontiguousarray(weights, np.float32)),
+        _p(None if shared is None else np.ascontiguousarray(shared, np.float32)),
+        _p(None if gl is None else np.ascontiguousarray(gl, np.float32)), rows, top_k, d, _p(out)) == 0
     return out
 
 

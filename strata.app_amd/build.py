@@ -18,7 +18,7 @@ BUILD = HERE / "_build"
 LIB = HERE / "libstrata_moe.so"
 INCLUDE = HERE.parent / "include"
 
-HIP_SOURCES = ["sm_route_group.hip", "sm_gemm.hip", "sm_wide.hip", "sm_post.hip", "sm_runtime.cpp"]
+HIP_SOURCES = ["sm_route_group.hip", "sm_gemm.hip", "sm_wide.hip", "sm_post.hip", "sm_decode.hip", "sm_runtime.cpp"]
 HOST_SOURCES = ["sm_synth.cpp", "sm_gguf.cpp", "sm_tiered.cpp"]
 
 HIPCC_FLAGS = [

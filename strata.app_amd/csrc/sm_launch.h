@@ -158,6 +158,59 @@ hipError_t launch_gate_logit(Fmt fmt, const _Float16* x, const uint8_t* gv, floa
 hipError_t launch_decode_rows(Fmt fmt, const uint8_t* w, uint32_t rows, uint32_t k, uint64_t row_bytes,
                               uint16_t* out, hipStream_t s);
 
+// ---- decode-side MoE (T <= 8 rows) ----
+// The first-appearance plan (MoePlan, 1620 bytes) of rows * top_k <= 80 entries; the launch
+// also copies up to two validated address tables (pinned host ring -> device snapshot).
+struct DecodePlanArgs {
+    const int32_t* ids;         // [rows * top_k]
+    const int32_t* resident;    // the layer's [E] residency row; null = full residency
+    float* usage;               // the layer's [E] usage row (tiered mode); null = none
+    uint8_t* plan;              // the layer's MoePlan
+    uint32_t* status;           // bit 1 on an id outside [0, E) (may be null)
+    uint32_t rows, top_k, n_experts;
+    const uint64_t* snap_src;
+    uint64_t* snap_dst;
+    uint32_t snap_words;
+    const uint64_t* snap_src2;
+    uint64_t* snap_dst2;
+    uint32_t snap_words2;
+};
+hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t s);
+// A standalone expert stage's snapshot copy (src may be null: nothing copied); clears *status.
+hipError_t launch_snapshot_copy(const uint64_t* src, uint64_t* dst, uint32_t words, uint32_t* status, hipStream_t s);
+// Q8_1 blocks (36 B: half d, half sum, int8 q[32]) of rows x n values (F16 or F32 input).
+hipError_t launch_quantize_q8_1(const void* x, bool f32_input, uint8_t* y, uint32_t n, uint32_t rows, hipStream_t s);
+// Grouped mat-vec of one stage over a MoePlan. gate/up: act = Q8_1 [rows][k/32] by token,
+// out0/out1 = gate/up F32 [n_entries][out_width] by grouped entry; down: act = Q8_1
+// [n_entries][k/32] by grouped entry, out0 = parts F32 [n_entries][out_width] by route index.
+struct DecodeMatvec {
+    const uint64_t* addresses;  // device [E][3]
+    const uint8_t* act;
+    const uint8_t* plan;
+    float* out0;
+    float* out1;
+    uint32_t* status;
+    uint32_t n_entries, n_experts, act_rows;
+    uint32_t k, out_width;
+    uint64_t row_bytes;
+};
+hipError_t launch_decode_matvec(Fmt fmt, bool gate_up, const DecodeMatvec& m, hipStream_t s);
+hipError_t launch_swiglu_f32(const float* gate, const float* up, float* out, uint64_t n, hipStream_t s);
+// The shared expert of a decode layer over F16/BF16 weights [n_out][k]. gate/up (w0 gate, w1 up,
+// x F16 [rows][k]): out = hidden F32 [rows][n_out] = silu(x.Wg) * (x.Wu). down (w0, x F32 hidden
+// [rows][k]): out F32 [rows][n_out] = x.Wd. k is a multiple of 64; rows <= 8.
+struct DenseDecode {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const void* x;
+    float* out;
+    uint32_t rows, k, n_out;
+};
+hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipStream_t s);
+// out = (p_0 w_0 + sum_r fma) + shared * sigmoid(gl); shared == null: no shared term.
+hipError_t launch_combine_decode(const float* parts, const float* w, const float* shared, const float* gl, float* out,
+                                 uint32_t rows, uint32_t top_k, uint32_t d, hipStream_t s);
+
 // ---- post ops ----
 hipError_t launch_swiglu(const float* gate, const float* up, _Float16* out, uint64_t n,
                          hipStream_t s);

@@ -1504,3 +1504,486 @@ sm_status sm_read_layer_status(sm_context* ctx, void* stream, sm_view plan, sm_v
 }
 
 }  // extern "C"
+
+// =========================================================================================
+// Decode-side MoE (the reference's Window MoE over T = 1..8 rows; moe_dispatch.hpp:13-372).
+// =========================================================================================
+namespace {
+
+// Rows and entries of the plan; widths as prefill (hidden a multiple of 256, the expert width of
+// 64). A K-quant down stage needs the expert width in whole 256-value super-blocks, which the
+// weight check reports.
+sm_status decode_shape_check(const sm_moe_shape* s, const char* prefix, std::string& err, bool need_ff) {
+    sm_status st = shape_check(s, prefix, err, need_ff);
+    if (st != SM_OK) return st;
+    if (s->rows > SM_DECODE_MAX_ROWS || uint64_t(s->rows) * s->top_k > SM_MOE_PLAN_MAX_ENTRIES) {
+        err = std::string(prefix) + " requires T=1..8 rows and at most 80 routed entries";
+        return SM_E_SHAPE;
+    }
+    return SM_OK;
+}
+
+// The selected layer's slice of a table view that starts at layer 0: validated over
+// [0, (layer + 1) * per_layer) and registered as the slice alone.
+bool layer_slice(Check& c, const sm_view& v, uint32_t layer, uint64_t per_layer, uint64_t align, const char* name,
+                 bool writable, uintptr_t& out) {
+    uint64_t need;
+    if (!mul_ok({uint64_t(layer) + 1u, per_layer}, need)) return c.fail(SM_E_SHAPE, c.prefix + " table size overflows");
+    uintptr_t base;
+    if (!c.view(v, need, align, name, writable, base)) return false;
+    auto& r = writable ? c.outputs.back() : c.inputs.back();
+    r.ptr = base + uint64_t(layer) * per_layer;
+    r.bytes = per_layer;
+    out = r.ptr;
+    return true;
+}
+
+struct DecodePlanRes { uintptr_t ids = 0, resident = 0, usage = 0, plan = 0, status = 0; };
+bool check_decode_plan(Check& c, const sm_moe_shape& s, const sm_moe_plan_buffers& b, DecodePlanRes& r, bool ids_view) {
+    const uint64_t n = uint64_t(s.rows) * s.top_k, E = s.n_experts;
+    if (ids_view && !c.view(b.ids, n * 4, 4, "route IDs", false, r.ids)) return false;
+    if (!layer_slice(c, b.plans, b.layer, SM_MOE_PLAN_BYTES, 4, "MoePlan", true, r.plan)) return false;
+    if (b.resident.buffer != 0 && !layer_slice(c, b.resident, b.layer, E * 4, 4, "residency table", false, r.resident))
+        return false;
+    if (b.usage.buffer != 0 && !layer_slice(c, b.usage, b.layer, E * 4, 4, "usage table", true, r.usage)) return false;
+    if (b.status.buffer != 0 && !c.view(b.status, 4, 4, "status", true, r.status)) return false;
+    return true;
+}
+
+// A read-only MoePlan of the selected layer.
+bool decode_plan_input(Check& c, const sm_view& plans, uint32_t layer, uintptr_t& out) {
+    return layer_slice(c, plans, layer, SM_MOE_PLAN_BYTES, 4, "MoePlan", false, out);
+}
+
+sm::DecodePlanArgs decode_plan_args(const sm_moe_shape& s, const DecodePlanRes& r) {
+    sm::DecodePlanArgs a{};
+    a.ids = reinterpret_cast<const int32_t*>(r.ids);
+    a.resident = reinterpret_cast<const int32_t*>(r.resident);
+    a.usage = reinterpret_cast<float*>(r.usage);
+    a.plan = reinterpret_cast<uint8_t*>(r.plan);
+    a.status = reinterpret_cast<uint32_t*>(r.status);
+    a.rows = s.rows;
+    a.top_k = s.top_k;
+    a.n_experts = s.n_experts;
+    return a;
+}
+
+uint64_t q81_bytes(uint64_t rows, uint64_t n) { return rows * (n / 32u) * SM_Q8_1_BLOCK_BYTES; }
+
+// One grouped mat-vec stage over a validated expert table: the snapshot copy (from a pinned
+// ring slot; it also clears the status word when `clear` is set) then the mat-vec. `slot` < -1
+// means the copy happens elsewhere (a decode layer's plan launch).
+struct DecodeStage { WeightsRes w; uintptr_t act = 0, plan = 0, out0 = 0, out1 = 0, status = 0; };
+sm::DecodeMatvec decode_matvec(const sm_moe_shape& s, int fmt, bool gate_up, const DecodeStage& r) {
+    sm::DecodeMatvec m{};
+    m.addresses = reinterpret_cast<const uint64_t*>(r.w.snapshot);
+    m.act = reinterpret_cast<const uint8_t*>(r.act);
+    m.plan = reinterpret_cast<const uint8_t*>(r.plan);
+    m.out0 = reinterpret_cast<float*>(r.out0);
+    m.out1 = reinterpret_cast<float*>(r.out1);
+    m.status = reinterpret_cast<uint32_t*>(r.status);
+    m.n_entries = s.rows * s.top_k;
+    m.n_experts = s.n_experts;
+    m.act_rows = gate_up ? s.rows : s.rows * s.top_k;
+    m.k = gate_up ? s.hidden : s.expert_ff;
+    m.out_width = gate_up ? s.expert_ff : s.hidden;
+    m.row_bytes = fmt_row_bytes(fmt, m.k);
+    return m;
+}
+
+sm_status encode_decode_stage(sm_segment* seg, const sm_moe_shape& s, int fmt, bool gate_up, const DecodeStage& r,
+                              bool clear_status) {
+    const int slot = claim_ring_slot(seg->ctx, r.w.table);
+    if (claim_status(slot) != SM_OK) return ring_fail(seg, claim_status(slot));
+    const uint64_t* src = slot >= 0 ? seg->ctx->ring + uint64_t(slot) * sm_context::kSlotWords : nullptr;
+    uint64_t* dst = reinterpret_cast<uint64_t*>(r.w.snapshot);
+    const uint32_t words = slot >= 0 ? uint32_t(r.w.table.size()) : 0u;
+    uint32_t* status = clear_status ? reinterpret_cast<uint32_t*>(r.status) : nullptr;
+    add_step(seg, gate_up ? "decode gate/up snapshot" : "decode down snapshot",
+             [=](hipStream_t st) { return sm::launch_snapshot_copy(src, dst, words, status, st); });
+    seg->steps.back().ring_slot = slot;
+    const sm::DecodeMatvec m = decode_matvec(s, fmt, gate_up, r);
+    add_step(seg, gate_up ? "decode gate/up" : "decode down",
+             [=](hipStream_t st) { return sm::launch_decode_matvec(Fmt(fmt), gate_up, m, st); });
+    return SM_OK;
+}
+
+bool check_decode_experts(Check& c, const sm_moe_shape& s, int fmt, const sm_expert_weights& w, const sm_view& act,
+                          const sm_view& plans, const sm_view& gate, const sm_view& up, const sm_view& status,
+                          DecodeStage& r, bool act_view, bool plan_view, bool status_view) {
+    if (!routed_fmt(fmt)) return c.fail(SM_E_FORMAT, c.prefix + " weight format is not a supported block format");
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    return check_weights(c, s, w, fmt, true, r.w) &&
+           (!act_view || c.view(act, q81_bytes(s.rows, s.hidden), 4, "Q8_1 activations", false, r.act)) &&
+           (!plan_view || decode_plan_input(c, plans, w.layer, r.plan)) &&
+           c.view(gate, N * s.expert_ff * 4, 16, "gate", true, r.out0) &&
+           c.view(up, N * s.expert_ff * 4, 16, "up", true, r.out1) &&
+           (!status_view || c.view(status, 4, 4, "status", true, r.status));
+}
+
+bool check_decode_down(Check& c, const sm_moe_shape& s, int fmt, const sm_expert_weights& w, const sm_view& act,
+                       const sm_view& plans, const sm_view& parts, const sm_view& status, DecodeStage& r, bool act_view,
+                       bool plan_view, bool status_view) {
+    if (!routed_fmt(fmt)) return c.fail(SM_E_FORMAT, c.prefix + " weight format is not a supported block format");
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    return check_weights(c, s, w, fmt, false, r.w) &&
+           (!act_view || c.view(act, q81_bytes(N, s.expert_ff), 4, "Q8_1 hidden", false, r.act)) &&
+           (!plan_view || decode_plan_input(c, plans, w.layer, r.plan)) &&
+           c.view(parts, N * s.hidden * 4, 16, "parts", true, r.out0) &&
+           (!status_view || c.view(status, 4, 4, "status", true, r.status));
+}
+
+void encode_q81_launch(sm_segment* seg, uintptr_t in, bool f32, uintptr_t out, uint32_t n, uint32_t rows,
+                       const char* label) {
+    add_step(seg, label, [=](hipStream_t st) {
+        return sm::launch_quantize_q8_1(reinterpret_cast<const void*>(in), f32, reinterpret_cast<uint8_t*>(out), n, rows, st);
+    });
+}
+
+void encode_swiglu_f32_launch(sm_segment* seg, uintptr_t g, uintptr_t u, uintptr_t o, uint64_t n) {
+    add_step(seg, "decode swiglu", [=](hipStream_t st) {
+        return sm::launch_swiglu_f32(reinterpret_cast<const float*>(g), reinterpret_cast<const float*>(u),
+                                     reinterpret_cast<float*>(o), n, st);
+    });
+}
+
+void encode_combine_decode_launch(sm_segment* seg, const sm_moe_shape& s, const CombineRes& r) {
+    const auto rows = s.rows, K = s.top_k, d = s.hidden;
+    add_step(seg, "decode combine", [=](hipStream_t st) {
+        return sm::launch_combine_decode(reinterpret_cast<const float*>(r.parts), reinterpret_cast<const float*>(r.weights),
+                                         reinterpret_cast<const float*>(r.shared), reinterpret_cast<const float*>(r.gate),
+                                         reinterpret_cast<float*>(r.out), rows, K, d, st);
+    });
+}
+
+// The decode shared expert over F16/BF16 weights: the hidden view holds F32 [T][Is] (the
+// reference's F32 shx SwiGLU output), Is a multiple of 64 (the reference model's 640 fits).
+bool check_shared_decode(Check& c, const sm_moe_shape& s, int fmt, const sm_shared_buffers& b, SharedRes& r) {
+    if (!dense_fmt(fmt)) return c.fail(SM_E_FORMAT, c.prefix + " shared expert format must be F16 or BF16");
+    const uint64_t Is = s.shared_ff;
+    if (Is == 0 || Is % 64 != 0) return c.fail(SM_E_SHAPE, c.prefix + " shared expert width must be a positive multiple of 64");
+    uint64_t x_b, w_b, h_b, o_b;
+    if (!mul_ok({s.rows, s.hidden, 2}, x_b) || !mul_ok({Is, s.hidden, 2}, w_b) || !mul_ok({s.rows, Is, 4}, h_b) ||
+        !mul_ok({s.rows, s.hidden, 4}, o_b))
+        return c.fail(SM_E_SHAPE, c.prefix + " buffer size overflows");
+    return c.view(b.mixed_h, x_b, 16, "mixed activation", false, r.x) &&
+           c.view(b.gate_weights, w_b, 16, "shared gate weights", false, r.wg) &&
+           c.view(b.up_weights, w_b, 16, "shared up weights", false, r.wu) &&
+           c.view(b.down_weights, w_b, 16, "shared down weights", false, r.wd) &&
+           c.view(b.gate_vector, uint64_t(s.hidden) * 2, 16, "shared gate vector", false, r.gv) &&
+           c.view(b.hidden, h_b, 16, "shared hidden", true, r.hidden) &&
+           c.view(b.output, o_b, 16, "shared output", true, r.out) &&
+           c.view(b.gate_logit, uint64_t(s.rows) * 4, 4, "shared gate logit", true, r.gl);
+}
+
+void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r) {
+    sm::DenseDecode gu{};
+    gu.w0 = reinterpret_cast<const uint8_t*>(r.wg);
+    gu.w1 = reinterpret_cast<const uint8_t*>(r.wu);
+    gu.x = reinterpret_cast<const void*>(r.x);
+    gu.out = reinterpret_cast<float*>(r.hidden);
+    gu.rows = s.rows;
+    gu.k = s.hidden;
+    gu.n_out = s.shared_ff;
+    sm::DenseDecode dn{};
+    dn.w0 = reinterpret_cast<const uint8_t*>(r.wd);
+    dn.x = reinterpret_cast<const void*>(r.hidden);
+    dn.out = reinterpret_cast<float*>(r.out);
+    dn.rows = s.rows;
+    dn.k = s.shared_ff;
+    dn.n_out = s.hidden;
+    const auto rows = s.rows, d = s.hidden;
+    const uintptr_t x = r.x, gv = r.gv, gl = r.gl;
+    add_step(seg, "decode shared gate/up", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), true, gu, st); });
+    add_step(seg, "decode shared down", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), false, dn, st); });
+    add_step(seg, "shared gate logit", [=](hipStream_t st) {
+        return sm::launch_gate_logit(Fmt(fmt), reinterpret_cast<const _Float16*>(x), reinterpret_cast<const uint8_t*>(gv),
+                                     reinterpret_cast<float*>(gl), rows, d, st);
+    });
+}
+
+// The routed FFN's scratch and output views (gate, up, hidden, Q8_1 hidden, parts, status).
+struct RoutedFFNRes { DecodeStage gu, dn; uintptr_t hidden = 0, hq = 0; };
+bool check_routed_ffn(Check& c, const sm_moe_shape& s, int fgu, int fdn, const sm_moe_routed_ffn_buffers& b,
+                      RoutedFFNRes& r, bool own_inputs) {
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    if (!check_decode_experts(c, s, fgu, b.gate_up_weights, b.input_activations, b.plans, b.gate, b.up, b.status, r.gu,
+                              own_inputs, own_inputs, true))
+        return false;
+    if (!c.view(b.hidden, N * s.expert_ff * 4, 16, "hidden", true, r.hidden) ||
+        !c.view(b.down_activations, q81_bytes(N, s.expert_ff), 4, "Q8_1 hidden", true, r.hq))
+        return false;
+    r.dn.act = r.hq;
+    r.dn.plan = r.gu.plan;
+    r.dn.status = r.gu.status;
+    return check_decode_down(c, s, fdn, b.down_weights, b.down_activations, b.plans, b.parts, b.status, r.dn, false, false,
+                             false);
+}
+
+// gate/up, SwiGLU, Q8_1, down. With snapshots_done, the plan launch has copied both address
+// tables and cleared the status word already (a decode layer).
+sm_status encode_routed_ffn_launch(sm_segment* seg, const sm_moe_shape& s, int fgu, int fdn, const RoutedFFNRes& r,
+                                   bool snapshots_done) {
+    const uint64_t N = uint64_t(s.rows) * s.top_k;
+    if (snapshots_done) {
+        const sm::DecodeMatvec m = decode_matvec(s, fgu, true, r.gu);
+        add_step(seg, "decode gate/up", [=](hipStream_t st) { return sm::launch_decode_matvec(Fmt(fgu), true, m, st); });
+    } else {
+        const sm_status st = encode_decode_stage(seg, s, fgu, true, r.gu, true);
+        if (st != SM_OK) return st;
+    }
+    encode_swiglu_f32_launch(seg, r.gu.out0, r.gu.out1, r.hidden, N * s.expert_ff);
+    encode_q81_launch(seg, r.hidden, true, r.hq, s.expert_ff, uint32_t(N), "decode Q8_1 hidden");
+    if (snapshots_done) {
+        const sm::DecodeMatvec m = decode_matvec(s, fdn, false, r.dn);
+        add_step(seg, "decode down", [=](hipStream_t st) { return sm::launch_decode_matvec(Fmt(fdn), false, m, st); });
+        return SM_OK;
+    }
+    return encode_decode_stage(seg, s, fdn, false, r.dn, false);
+}
+
+}  // namespace
+
+extern "C" {
+
+sm_status sm_encode_moe_plan(sm_segment* seg, const sm_moe_shape* shape, const sm_moe_plan_buffers* b) {
+    Check c;
+    const char* P = "MoE plan";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    DecodePlanRes r;
+    if (!check_decode_plan(c, *shape, *b, r, true) || !c.aliases()) return finish(seg, c);
+    const sm::DecodePlanArgs a = decode_plan_args(*shape, r);
+    add_step(seg, "decode plan", [=](hipStream_t s) { return sm::launch_decode_plan(a, s); });
+    return SM_OK;
+}
+
+sm_status sm_encode_quantize_q8_1(sm_segment* seg, uint32_t rows, uint32_t n, int f32_input, sm_view input,
+                                  sm_view output) {
+    Check c;
+    const char* P = "Q8_1 quantize";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    if (rows == 0 || rows > SM_MOE_PLAN_MAX_ENTRIES * 8u || n == 0 || n % 32 != 0)
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " needs 1..640 rows of a positive multiple of 32 values");
+    uintptr_t in, out;
+    const uint64_t es = f32_input ? 4 : 2;
+    if (!c.view(input, uint64_t(rows) * n * es, es, "input", false, in) ||
+        !c.view(output, q81_bytes(rows, n), 4, "Q8_1 output", true, out) || !c.aliases())
+        return finish(seg, c);
+    encode_q81_launch(seg, in, f32_input != 0, out, n, rows, "Q8_1 quantize");
+    return SM_OK;
+}
+
+sm_status sm_encode_moe_experts(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                                const sm_moe_expert_buffers* b) {
+    Check c;
+    const char* P = "MoE experts";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, true)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    DecodeStage r;
+    if (!check_decode_experts(c, *shape, fmt, b->weights, b->activations, b->plans, b->gate, b->up, b->status, r, true,
+                              true, true) ||
+        !c.aliases())
+        return finish(seg, c);
+    return encode_decode_stage(seg, *shape, fmt, true, r, true);
+}
+
+sm_status sm_encode_moe_down(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt, const sm_moe_down_buffers* b) {
+    Check c;
+    const char* P = "MoE down";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, true)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    DecodeStage r;
+    if (!check_decode_down(c, *shape, fmt, b->weights, b->activations, b->plans, b->parts, b->status, r, true, true, true) ||
+        !c.aliases())
+        return finish(seg, c);
+    return encode_decode_stage(seg, *shape, fmt, false, r, true);
+}
+
+sm_status sm_encode_moe_swiglu(sm_segment* seg, uint32_t rows, uint32_t width, const sm_moe_swiglu_buffers* b) {
+    Check c;
+    const char* P = "MoE SwiGLU";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    if (rows == 0 || rows > SM_MOE_PLAN_MAX_ENTRIES || width == 0)
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " needs 1..80 rows of a positive width");
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    const uint64_t n = uint64_t(rows) * width;
+    uintptr_t g, u, o;
+    if (!c.view(b->gate, n * 4, 4, "gate", false, g) || !c.view(b->up, n * 4, 4, "up", false, u) ||
+        !c.view(b->output, n * 4, 4, "output", true, o) || !c.aliases())
+        return finish(seg, c);
+    encode_swiglu_f32_launch(seg, g, u, o, n);
+    return SM_OK;
+}
+
+sm_status sm_encode_moe_routed_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format gate_up_fmt,
+                                   sm_format down_fmt, const sm_moe_routed_ffn_buffers* b) {
+    Check c;
+    const char* P = "MoE routed FFN";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, true)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    if (b->gate_up_weights.layer != b->down_weights.layer)
+        return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " gate/up and down weights select different layers");
+    RoutedFFNRes r;
+    if (!check_routed_ffn(c, *shape, gate_up_fmt, down_fmt, *b, r, true) || !c.aliases()) return finish(seg, c);
+    return encode_routed_ffn_launch(seg, *shape, gate_up_fmt, down_fmt, r, false);
+}
+
+sm_status sm_encode_moe_combine(sm_segment* seg, const sm_moe_shape* shape, const sm_combine_buffers* b) {
+    Check c;
+    const char* P = "MoE combine";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    CombineRes r{};
+    if (!check_combine(c, *shape, *b, r) || !c.aliases()) return finish(seg, c);
+    encode_combine_decode_launch(seg, *shape, r);
+    return SM_OK;
+}
+
+sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape, const sm_layer_formats* f,
+                                     const sm_decode_layer_buffers* b) {
+    Check c;
+    const char* P = "MoE decode layer";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, true)) != SM_OK) return record_fail(seg, st, err);
+    if (!b || !f) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers or formats are null");
+    const sm_moe_shape& s = *shape;
+    const sm_moe_routed_ffn_buffers& rb = b->routed;
+    if (rb.gate_up_weights.layer != b->layer || rb.down_weights.layer != b->layer)
+        return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " expert weights select a different layer than the plan");
+    // Route: router GEMM into the logits, top-k in multiply mode.
+    RouterRes rr{};
+    uint64_t x_b, w_b;
+    if (!mul_ok({s.rows, s.hidden, 2}, x_b) || !mul_ok({s.n_experts, s.hidden, 4}, w_b))
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " buffer size overflows");
+    bool ok = c.view(b->mixed_h, x_b, 16, "mixed activation", false, rr.x) &&
+              c.view(b->router_weights, w_b, 16, "router weights", false, rr.w);
+    rr.bias = 0;
+    if (ok && b->router_bias.buffer != 0)
+        ok = c.view(b->router_bias, uint64_t(s.n_experts) * 4, 4, "router bias", false, rr.bias);
+    RouteRes ro{};
+    const sm_route_buffers rob{b->logits, b->route_ids, b->route_weights};
+    ok = ok && check_route(c, s, rob, ro, false);
+    rr.logits = ro.logits;
+    // Plan (reads the route ids written above) and the Q8_1 input.
+    DecodePlanRes pr;
+    pr.ids = ro.ids;
+    // (The status word is registered once, by the routed FFN below; the plan launch clears it.)
+    const sm_moe_plan_buffers pb{b->route_ids, b->resident, b->usage, b->plans, sm_view{}, b->layer};
+    ok = ok && check_decode_plan(c, s, pb, pr, false);
+    uintptr_t xq = 0;
+    ok = ok && c.view(b->input_activations, q81_bytes(s.rows, s.hidden), 4, "Q8_1 activations", true, xq);
+    // Routed FFN over that plan and input; its status word is the plan's.
+    RoutedFFNRes fr;
+    ok = ok && check_routed_ffn(c, s, f->gate_up, f->down, rb, fr, false);
+    fr.gu.act = xq;
+    fr.gu.plan = fr.dn.plan = pr.plan;
+    pr.status = fr.gu.status;
+    // Shared expert (optional) and combine.
+    SharedRes sr{};
+    if (ok && s.shared_ff != 0) {
+        if (b->shared.mixed_h.buffer != b->mixed_h.buffer || b->shared.mixed_h.offset != b->mixed_h.offset)
+            return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " shared expert must read the layer's mixed activation");
+        ok = check_shared_decode(c, s, f->shared, b->shared, sr);
+    }
+    CombineRes cr{};
+    if (ok) {
+        uint64_t o_b;
+        if (!mul_ok({s.rows, s.hidden, 4}, o_b)) return record_fail(seg, SM_E_SHAPE, std::string(P) + " buffer size overflows");
+        cr.parts = fr.dn.out0;
+        cr.weights = ro.weights;
+        cr.shared = s.shared_ff != 0 ? sr.out : 0;
+        cr.gate = s.shared_ff != 0 ? sr.gl : 0;
+        ok = c.view(b->output, o_b, 16, "output", true, cr.out);
+    }
+    if (!ok || !c.aliases()) return finish(seg, c);
+    // Launches: the plan launch also copies both validated address tables.
+    const int s_gu = claim_ring_slot(seg->ctx, fr.gu.w.table);
+    if (claim_status(s_gu) != SM_OK) return ring_fail(seg, claim_status(s_gu));
+    const int s_dn = claim_ring_slot(seg->ctx, fr.dn.w.table);
+    if (claim_status(s_dn) != SM_OK) {
+        if (s_gu >= 0) {
+            std::lock_guard<std::mutex> lk(seg->ctx->ring_mu);
+            seg->ctx->ring_claimed[s_gu] = false;
+        }
+        return ring_fail(seg, claim_status(s_dn));
+    }
+    const auto rows = s.rows, d = s.hidden, E = s.n_experts;
+    add_step(seg, "router GEMM", [=](hipStream_t st2) {
+        return sm::launch_router_gemm(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
+                                      reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits), rows,
+                                      d, E, st2);
+    });
+    encode_route_launch(seg, s, 0, ro);  // multiply mode (the Window's route)
+    sm::DecodePlanArgs pa = decode_plan_args(s, pr);
+    pa.snap_src = s_gu >= 0 ? seg->ctx->ring + uint64_t(s_gu) * sm_context::kSlotWords : nullptr;
+    pa.snap_dst = reinterpret_cast<uint64_t*>(fr.gu.w.snapshot);
+    pa.snap_words = s_gu >= 0 ? uint32_t(fr.gu.w.table.size()) : 0u;
+    pa.snap_src2 = s_dn >= 0 ? seg->ctx->ring + uint64_t(s_dn) * sm_context::kSlotWords : nullptr;
+    pa.snap_dst2 = reinterpret_cast<uint64_t*>(fr.dn.w.snapshot);
+    pa.snap_words2 = s_dn >= 0 ? uint32_t(fr.dn.w.table.size()) : 0u;
+    add_step(seg, "decode plan", [=](hipStream_t st2) { return sm::launch_decode_plan(pa, st2); });
+    seg->steps.back().ring_slot = s_gu;
+    seg->steps.back().ring_slot2 = s_dn;
+    encode_q81_launch(seg, rr.x, false, xq, s.hidden, s.rows, "decode Q8_1 input");
+    if ((st = encode_routed_ffn_launch(seg, s, f->gate_up, f->down, fr, true)) != SM_OK) return st;
+    if (s.shared_ff != 0) encode_shared_decode_launch(seg, s, f->shared, sr);
+    encode_combine_decode_launch(seg, s, cr);
+    return SM_OK;
+}
+
+sm_status sm_encode_moe_shared_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
+                                   const sm_moe_shared_ffn_buffers* b) {
+    Check c;
+    const char* P = "MoE shared FFN";
+    sm_status st = begin_check(seg, P, c);
+    if (st != SM_OK) return st;
+    std::string err;
+    if ((st = decode_shape_check(shape, P, err, false)) != SM_OK) return record_fail(seg, st, err);
+    if (!b) return record_fail(seg, SM_E_ARGUMENT, std::string(P) + " buffers are null");
+    SharedRes sr{};
+    CombineRes cr{};
+    uint64_t p_b, w_b, o_b;
+    if (!mul_ok({shape->rows, shape->top_k, shape->hidden, 4}, p_b) || !mul_ok({shape->rows, shape->top_k, 4}, w_b) ||
+        !mul_ok({shape->rows, shape->hidden, 4}, o_b))
+        return record_fail(seg, SM_E_SHAPE, std::string(P) + " buffer size overflows");
+    // The combine reads the shared output and gate logit this call writes (registered once, as
+    // the shared stage's outputs).
+    if (!check_shared_decode(c, *shape, fmt, b->shared, sr) ||
+        !c.view(b->routed_parts, p_b, 16, "routed parts", false, cr.parts) ||
+        !c.view(b->route_weights, w_b, 4, "route weights", false, cr.weights) ||
+        !c.view(b->output, o_b, 16, "output", true, cr.out) || !c.aliases())
+        return finish(seg, c);
+    cr.shared = sr.out;
+    cr.gate = sr.gl;
+    encode_shared_decode_launch(seg, *shape, fmt, sr);
+    encode_combine_decode_launch(seg, *shape, cr);
+    return SM_OK;
+}
+
+sm_status sm_submit_moe_decode_layer(sm_context* ctx, void* stream, const sm_moe_shape* shape,
+                                     const sm_layer_formats* formats, const sm_decode_layer_buffers* b, char* err,
+                                     size_t cap) {
+    SM_SUBMIT_BODY(sm_encode_moe_decode_layer(seg, shape, formats, b))
+}
+
+}  // extern "C"

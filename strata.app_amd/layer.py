@@ -262,6 +262,118 @@ class PromptWorkspace:
         return self.chunk.read_status(stream)
 
 
+# Decode-side layers (the Window MoE, T <= 8 rows). The first two are the reference model's own
+# widths (d 2560, 512 experts top-10, expert and shared width 640) and share one seed, so their
+# weights are the same and T=1's input is T=8's first row; the last two are the prefill
+# configurations 2 and 4 at decode row counts (the step after prefill on the same layer).
+DECODE_CONFIGS = {
+    "window_t1": LayerConfig("window_t1", 1, 2560, 512, 10, 640, 640, moe.Q4_K, moe.Q8_0, moe.F16,
+                             seed=SEED_BASE + 28),
+    "window_t8": LayerConfig("window_t8", 8, 2560, 512, 10, 640, 640, moe.Q4_K, moe.Q8_0, moe.F16,
+                             seed=SEED_BASE + 28),
+    "full_layer_t8": LayerConfig("full_layer_t8", 8, 2048, 512, 10, 512, 512, moe.Q4_K, moe.Q8_0, moe.F16,
+                                 seed=SEED_BASE + 32),
+    "low_bit_t4": LayerConfig("low_bit_t4", 4, 4096, 256, 8, 1536, 1536, moe.Q2_K, moe.Q4_K, moe.BF16,
+                              seed=SEED_BASE + 44),
+}
+
+
+class DecodeWorkspace:
+    """Device buffers and C-ABI structs of one decode layer call (T <= 8 rows): the route, the
+    MoePlan (one layer), the Q8_1 input, the routed FFN's scratch, the shared expert and the
+    output (sm_encode_moe_decode_layer)."""
+
+    def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0"):
+        import torch
+        self.ctx, self.cfg, self.inputs = ctx, cfg, inputs
+        T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
+        N = T * K
+        self.shape = cfg.shape()
+        dev = torch.device(device)
+
+        def empty(nbytes, dtype=torch.uint8):
+            return torch.empty(nbytes // torch.tensor([], dtype=dtype).element_size(), dtype=dtype, device=dev)
+
+        reg = ctx.register
+        self.x = reg(_dev(inputs.x[:T].view(np.uint16).view(np.int16), dev))
+        self.w_router = reg(_dev(inputs.w_router, dev))
+        self.bias = reg(_dev(inputs.bias, dev)) if inputs.bias is not None else None
+        self.logits = reg(empty(T * E * 4, torch.float32))
+        self.ids = reg(empty(N * 4, torch.int32))
+        self.route_w = reg(empty(N * 4, torch.float32))
+        self.plans = reg(empty(moe.MOE_PLAN_BYTES, torch.int32))
+        self.xq = reg(empty(moe.q8_1_bytes(T, d), torch.int32))
+        self.gate = reg(empty(N * I * 4, torch.float32))
+        self.up = reg(empty(N * I * 4, torch.float32))
+        self.hidden = reg(empty(N * I * 4, torch.float32))
+        self.hq = reg(empty(moe.q8_1_bytes(N, I), torch.int32))
+        self.parts = reg(empty(N * d * 4, torch.float32))
+        self.status = reg(torch.zeros(1, dtype=torch.int32, device=dev))
+        self.snap_gu = reg(empty(E * 3 * 8, torch.int64))
+        self.snap_dn = reg(empty(E * 3 * 8, torch.int64))
+        self.out = reg(empty(T * d * 4, torch.float32))
+        self.w_gate = reg(_dev(inputs.w_gate, dev))
+        self.w_up = reg(_dev(inputs.w_up, dev))
+        self.w_down = reg(_dev(inputs.w_down, dev))
+        addr = []
+        for e in range(E):
+            addr += [self.w_gate.ptr + e * inputs.gu_stride, self.w_up.ptr + e * inputs.gu_stride,
+                     self.w_down.ptr + e * inputs.dn_stride]
+        self.addresses = addr
+        self.gu_table = moe.ExpertTable(addr, self.snap_gu.view(), [self.w_gate.view(), self.w_up.view()])
+        self.dn_table = moe.ExpertTable(addr, self.snap_dn.view(), [self.w_down.view()])
+        if Is:
+            self.sh_gate = reg(_dev(inputs.sh_gate, dev))
+            self.sh_up = reg(_dev(inputs.sh_up, dev))
+            self.sh_down = reg(_dev(inputs.sh_down, dev))
+            self.sh_gvec = reg(_dev(inputs.sh_gvec, dev))
+            self.sh_hidden = reg(empty(T * Is * 4, torch.float32))
+            self.sh_out = reg(empty(T * d * 4, torch.float32))
+            self.sh_gl = reg(empty(T * 4, torch.float32))
+        self.formats = moe.LayerFormats(cfg.gate_up_fmt, cfg.down_fmt, cfg.shared_fmt)
+
+    def routed_buffers(self) -> moe.MoeRoutedFFNBuffers:
+        return moe.MoeRoutedFFNBuffers(self.gu_table.struct, self.dn_table.struct, self.xq.view(), self.plans.view(),
+                                       self.gate.view(), self.up.view(), self.hidden.view(), self.hq.view(),
+                                       self.parts.view(), self.status.view())
+
+    def shared_buffers(self) -> moe.SharedBuffers:
+        if not self.cfg.shared_ff:
+            return moe.SharedBuffers()
+        return moe.SharedBuffers(self.x.view(), self.sh_gate.view(), self.sh_up.view(), self.sh_down.view(),
+                                 self.sh_gvec.view(), self.sh_hidden.view(), self.sh_out.view(), self.sh_gl.view())
+
+    def layer_buffers(self, resident: moe.View = moe.NULL_VIEW, usage: moe.View = moe.NULL_VIEW):
+        return moe.DecodeLayerBuffers(
+            self.x.view(), self.w_router.view(), self.bias.view() if self.bias is not None else moe.NULL_VIEW,
+            self.logits.view(), self.ids.view(), self.route_w.view(), resident, usage, self.plans.view(), 0,
+            self.xq.view(), self.routed_buffers(), self.shared_buffers(), self.out.view())
+
+    def encode(self, seg: moe.Segment, **kw):
+        self._lb = self.layer_buffers(**kw)
+        return seg.encode_moe_decode_layer(self.shape, self.formats, self._lb, keep=self)
+
+    def run(self, stream=0, **kw) -> None:
+        seg = self.ctx.segment()
+        ok, err = self.encode(seg, **kw)
+        if not ok:
+            seg.abort()
+            raise RuntimeError(err)
+        seg.commit(stream)
+
+    def read_status(self) -> int:
+        return int(self.status.tensor.cpu().item())
+
+
+def decode_weight_bytes(cfg: LayerConfig, n_active: int) -> int:
+    """Weight bytes a decode layer streams: the active experts' gate, up and down matrices, the
+    shared expert, and the router."""
+    d, I, Is, E = cfg.hidden, cfg.expert_ff, cfg.shared_ff, cfg.n_experts
+    routed = n_active * (2 * I * moe.row_bytes(cfg.gate_up_fmt, d) + d * moe.row_bytes(cfg.down_fmt, I))
+    shared = 3 * Is * d * 2 + d * 2 if Is else 0
+    return routed + shared + E * d * 4
+
+
 def layer_flops(cfg: LayerConfig) -> float:
     """Algorithmic FLOPs of one layer call (router, gate/up, down, shared)."""
     T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
@@ -273,5 +385,5 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
-__all__ = ["LayerConfig", "CONFIGS", "HostInputs", "make_inputs", "LayerWorkspace", "PromptWorkspace",
-           "layer_flops", "zipf_bias"]
+__all__ = ["LayerConfig", "CONFIGS", "DECODE_CONFIGS", "HostInputs", "make_inputs", "LayerWorkspace",
+           "PromptWorkspace", "DecodeWorkspace", "decode_weight_bytes", "layer_flops", "zipf_bias"]

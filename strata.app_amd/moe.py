@@ -49,6 +49,10 @@ EXPORTS = (
     "sm_gguf_load_experts", "sm_expert_slot_bytes", "sm_expert_store_create", "sm_expert_store_destroy",
     "sm_lease_set_create", "sm_lease_set_destroy", "sm_lease_set_retire_layer", "sm_lease_set_pins",
     "sm_expert_store_resolve_layer",
+    "sm_encode_moe_plan", "sm_encode_quantize_q8_1", "sm_encode_moe_experts", "sm_encode_moe_down",
+    "sm_encode_moe_swiglu", "sm_encode_moe_routed_ffn", "sm_encode_moe_combine", "sm_encode_moe_shared_ffn",
+    "sm_encode_moe_decode_layer",
+    "sm_submit_moe_decode_layer",
     "sm_synth_normal_f32", "sm_synth_normal_f16", "sm_synth_normal_bf16", "sm_quantize",
     "sm_synth_quantized",
 )
@@ -123,6 +127,49 @@ class LayerBuffers(C.Structure):
     _fields_ = [("route_gather", RouteGatherBuffers), ("shared", SharedBuffers),
                 ("gate_up", GateUpBuffers), ("down", DownBuffers),
                 ("combine", CombineBuffers)]
+
+
+# ---- decode-side MoE (the Window MoE over T <= 8 rows) ----------------------------------------
+DECODE_MAX_ROWS = 8
+MOE_PLAN_BYTES = 1620
+MOE_PLAN_MAX_ENTRIES = 80
+Q8_1_BLOCK_BYTES = 36
+
+
+class MoePlanBuffers(C.Structure):
+    _fields_ = [("ids", View), ("resident", View), ("usage", View), ("plans", View), ("status", View),
+                ("layer", C.c_uint32)]
+
+
+class MoeExpertBuffers(C.Structure):
+    _fields_ = [("weights", ExpertWeights), ("activations", View), ("plans", View), ("gate", View),
+                ("up", View), ("status", View)]
+
+
+class MoeDownBuffers(C.Structure):
+    _fields_ = [("weights", ExpertWeights), ("activations", View), ("plans", View), ("parts", View),
+                ("status", View)]
+
+
+class MoeRoutedFFNBuffers(C.Structure):
+    _fields_ = [("gate_up_weights", ExpertWeights), ("down_weights", ExpertWeights),
+                ("input_activations", View), ("plans", View), ("gate", View), ("up", View),
+                ("hidden", View), ("down_activations", View), ("parts", View), ("status", View)]
+
+
+class MoeSharedFFNBuffers(C.Structure):
+    _fields_ = [("shared", SharedBuffers), ("routed_parts", View), ("route_weights", View), ("output", View)]
+
+
+class DecodeLayerBuffers(C.Structure):
+    _fields_ = [("mixed_h", View), ("router_weights", View), ("router_bias", View), ("logits", View),
+                ("route_ids", View), ("route_weights", View), ("resident", View), ("usage", View),
+                ("plans", View), ("layer", C.c_uint32), ("input_activations", View),
+                ("routed", MoeRoutedFFNBuffers), ("shared", SharedBuffers), ("output", View)]
+
+
+def q8_1_bytes(rows: int, n: int) -> int:
+    return rows * (n // 32) * Q8_1_BLOCK_BYTES
 
 
 class GgufTensor(C.Structure):
@@ -230,6 +277,18 @@ def library() -> C.CDLL:
         "sm_submit_prefill_moe_chunks": (I, [P, P, C.POINTER(ChunkSchedule), C.POINTER(Shape),
                                              C.POINTER(LayerFormats), View, View, C.POINTER(LayerBuffers),
                                              C.c_char_p, C.c_size_t]),
+        "sm_encode_moe_plan": (I, [P, C.POINTER(Shape), C.POINTER(MoePlanBuffers)]),
+        "sm_encode_quantize_q8_1": (I, [P, U32, U32, I, View, View]),
+        "sm_encode_moe_experts": (I, [P, C.POINTER(Shape), I, C.POINTER(MoeExpertBuffers)]),
+        "sm_encode_moe_down": (I, [P, C.POINTER(Shape), I, C.POINTER(MoeDownBuffers)]),
+        "sm_encode_moe_swiglu": (I, [P, U32, U32, C.POINTER(SwiGLUBuffers)]),
+        "sm_encode_moe_routed_ffn": (I, [P, C.POINTER(Shape), I, I, C.POINTER(MoeRoutedFFNBuffers)]),
+        "sm_encode_moe_combine": (I, [P, C.POINTER(Shape), C.POINTER(CombineBuffers)]),
+        "sm_encode_moe_shared_ffn": (I, [P, C.POINTER(Shape), I, C.POINTER(MoeSharedFFNBuffers)]),
+        "sm_encode_moe_decode_layer": (I, [P, C.POINTER(Shape), C.POINTER(LayerFormats),
+                                           C.POINTER(DecodeLayerBuffers)]),
+        "sm_submit_moe_decode_layer": (I, [P, P, C.POINTER(Shape), C.POINTER(LayerFormats),
+                                           C.POINTER(DecodeLayerBuffers), C.c_char_p, C.c_size_t]),
         "sm_synth_normal_f32": (None, [U64, U64, C.c_float, P, U64]),
         "sm_synth_normal_f16": (None, [U64, U64, C.c_float, P, U64]),
         "sm_synth_normal_bf16": (None, [U64, U64, C.c_float, P, U64]),
@@ -545,6 +604,41 @@ class Segment:
         self._keep.append((schedule, keep))
         return self._ret(self.lib.sm_encode_prefill_moe_chunks(self.handle, C.byref(schedule), C.byref(shape),
                                                                C.byref(formats), input, output, C.byref(b)))
+
+    # Decode side (namespace strata::metal, moe_dispatch.hpp):
+    def encode_moe_plan(self, shape: Shape, b: MoePlanBuffers):
+        return self._ret(self.lib.sm_encode_moe_plan(self.handle, C.byref(shape), C.byref(b)))
+
+    def encode_quantize_q8_1(self, rows: int, n: int, f32_input: bool, input: View, output: View):
+        return self._ret(self.lib.sm_encode_quantize_q8_1(self.handle, rows, n, int(f32_input), input, output))
+
+    def encode_moe_experts(self, shape: Shape, fmt: int, b: MoeExpertBuffers, keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_moe_experts(self.handle, C.byref(shape), fmt, C.byref(b)))
+
+    def encode_moe_down(self, shape: Shape, fmt: int, b: MoeDownBuffers, keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_moe_down(self.handle, C.byref(shape), fmt, C.byref(b)))
+
+    def encode_moe_swiglu(self, rows: int, width: int, b: SwiGLUBuffers):
+        return self._ret(self.lib.sm_encode_moe_swiglu(self.handle, rows, width, C.byref(b)))
+
+    def encode_moe_routed_ffn(self, shape: Shape, gate_up_fmt: int, down_fmt: int, b: MoeRoutedFFNBuffers,
+                              keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_moe_routed_ffn(self.handle, C.byref(shape), gate_up_fmt, down_fmt,
+                                                           C.byref(b)))
+
+    def encode_moe_combine(self, shape: Shape, b: CombineBuffers):
+        return self._ret(self.lib.sm_encode_moe_combine(self.handle, C.byref(shape), C.byref(b)))
+
+    def encode_moe_shared_ffn(self, shape: Shape, fmt: int, b: MoeSharedFFNBuffers):
+        return self._ret(self.lib.sm_encode_moe_shared_ffn(self.handle, C.byref(shape), fmt, C.byref(b)))
+
+    def encode_moe_decode_layer(self, shape: Shape, formats: LayerFormats, b: DecodeLayerBuffers, keep=None):
+        self._keep.append(keep)
+        return self._ret(self.lib.sm_encode_moe_decode_layer(self.handle, C.byref(shape), C.byref(formats),
+                                                             C.byref(b)))
 
     def encode_prefill_dequant(self, fmt: int, n_out: int, k: int, weights: View, k_major_f16: View):
         return self._ret(self.lib.sm_encode_dequant(self.handle, fmt, n_out, k, weights, k_major_f16))
