@@ -212,6 +212,67 @@ def measure_route(moe, layer, ctx, steps: int):
     return out
 
 
+def measure_decode(moe, layer, ctx, name: str, steps: int, inputs=None):
+    """A decode layer (T <= 8 rows): whole-layer calls (encode + validate + commit each step), then
+    each launch on its own with HIP events around it on the caller's stream. The grouped mat-vecs
+    stream the active experts' weights once per group: their figure is weight bytes / kernel time
+    against the HBM peak."""
+    import numpy as np
+    import torch
+    cfg = layer.DECODE_CONFIGS[name]
+    T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
+    N = T * K
+    inp = inputs if inputs is not None else layer.make_inputs(cfg)
+    ws = layer.DecodeWorkspace(ctx, cfg, inp)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    lb = ws.layer_buffers()
+
+    def encode(seg):
+        return seg.encode_moe_decode_layer(ws.shape, ws.formats, lb)
+
+    for _ in range(10):
+        s = ctx.segment(); ok, err = encode(s); assert ok, err; s.commit(sh)
+    torch.cuda.synchronize()
+    if ws.read_status() != 0:
+        raise RuntimeError(f"decode layer status {ws.read_status()}")
+    n = max(50, steps * 10)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(n):
+        s = ctx.segment(); ok, err = encode(s); assert ok, err; s.commit(sh)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / n
+    acc = {}
+    for i in range(max(10, steps) + 2):
+        s = ctx.segment(); ok, err = encode(s); assert ok, err
+        for label, v in s.commit_timed(sh):
+            if i >= 2:
+                acc.setdefault(label, []).append(v)
+    us = {k: sum(v) / len(v) * 1e3 for k, v in acc.items()}
+    n_groups = int(ws.plans.tensor.cpu().numpy().view(np.uint32)[0])
+    gu_w = n_groups * 2 * I * moe.row_bytes(cfg.gate_up_fmt, d)
+    dn_w = n_groups * d * moe.row_bytes(cfg.down_fmt, I)
+    sh_w = 3 * Is * d * 2
+    fig = lambda b_, u_: {"kernel_us": round(u_, 2), "weight_bytes": b_, "gbs": round(b_ / u_ / 1e3, 1),  # noqa: E731
+                          "frac": round(b_ / u_ / 1e3 / HBM_PEAK_GBS, 4)}
+    out = {
+        "workload": f"decode:{cfg.name}", "tokens": T, "hidden": d, "experts": E, "top_k": K, "expert_ff": I,
+        "shared_ff": Is, "gate_up": moe.FORMAT_NAMES[cfg.gate_up_fmt], "down": moe.FORMAT_NAMES[cfg.down_fmt],
+        "active_experts": n_groups, "ms_per_layer": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1),
+        "layer_weight_gbs": round(layer.decode_weight_bytes(cfg, n_groups) / (ms / 1e3) / 1e9, 1),
+        "kernels_us": {k: round(v, 2) for k, v in us.items()},
+        "sum_kernels_us": round(sum(us.values()), 2),
+        "gate_up_matvec": fig(gu_w, us["decode gate/up"]),
+        "down_matvec": fig(dn_w, us["decode down"]),
+    }
+    if Is:
+        out["shared_matvecs"] = fig(sh_w, us["decode shared gate/up"] + us["decode shared down"])
+    log(f"decode {name}: {out}")
+    return out, inp
+
+
 def cpu_description() -> dict:
     """The host the CPU baseline ran on: model name, logical CPUs, NUMA nodes."""
     model = "unknown"
@@ -240,6 +301,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the configuration-3 (T=8192) grouped-GEMM figures")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode-layer figures (T = 1 and 8 at the reference model's widths)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 512 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -257,6 +320,11 @@ def main() -> int:
     pkg = ge.load_package()
     moe, layer = pkg.moe, pkg.layer
     ctx = moe.Context(0)
+    if args.decode_only:
+        d8, dinp = measure_decode(moe, layer, ctx, "window_t8", args.steps)
+        d1, _ = measure_decode(moe, layer, ctx, "window_t1", args.steps, inputs=dinp)
+        print(json.dumps({"decode": {"t1": d1, "t8": d8}}), flush=True)
+        return 0
     m = measure(moe, layer, ctx, args.config, args.steps, args.warmup, detailed=True)
     cfg, inp = m["cfg"], m["inp"]
     T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
@@ -337,6 +405,13 @@ def main() -> int:
                            "mfma_frac": round(d4 / F16_MFMA_PEAK_TFLOPS, 4)},
         }
         log(f"config 4: {extra['config4']}")
+
+    # ---- decode-side MoE (T = 1 and 8 rows at the reference model's widths) ----
+    if args.config == 2 and not args.no_config3:
+        d8, dinp = measure_decode(moe, layer, ctx, "window_t8", args.steps)
+        d1, _ = measure_decode(moe, layer, ctx, "window_t1", args.steps, inputs=dinp)
+        extra["decode"] = {"t1": d1, "t8": d8}
+        del dinp
 
     # ---- CPU baseline: the C++ restatement of the same stages on a bounded sample ----
     cpu = None

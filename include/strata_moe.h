@@ -295,12 +295,14 @@ sm_status sm_encode_full_layer(sm_segment* seg, const sm_moe_shape* shape,
  * a first-appearance expert plan, Q8_1 activations, grouped mat-vecs that read each active
  * expert's weights once per group, an F32 SwiGLU and the decode combine. The expert formats
  * are this library's block formats (Q8_0, Q4_K, Q2_K) over the same [layer][E][3] address
- * table as prefill. hidden is a multiple of 256 and expert_ff of 64 (K-quant down weights need
+ * table as prefill. hidden is a multiple of 256 and expert_ff of 64, both at most 4096 (K-quant down weights need
  * expert_ff in whole 256-value super-blocks; the reference model's 2560 / 640 fit); rows * top_k <= 80.
  * Status word (one per coordinator call, cleared on the GPU first): bit 0 an active expert's
  * address is null, bit 1 the plan is unusable (an id outside [0, E), a malformed header or
- * entry), bit 2 an active expert's tiered slot is not leased. Failing groups write zeros. */
+ * entry, a group of more than T entries), bit 2 an active expert's tiered slot is not leased.
+ * Failing groups write zeros. */
 #define SM_DECODE_MAX_ROWS 8u
+#define SM_DECODE_MAX_WIDTH 4096u       /* hidden and expert_ff of the decode mat-vecs          */
 #define SM_MOE_PLAN_BYTES 1620u       /* MoePlan, moe.metal:101-111 (TieredMoePlan, tiered.hpp:24-36) */
 #define SM_MOE_PLAN_MAX_ENTRIES 80u   /* T * k <= 8 * 10                                        */
 #define SM_Q8_1_BLOCK_BYTES 36u       /* Q81 {half d, half sum; int8 q[32]}, types.h:128-131     */

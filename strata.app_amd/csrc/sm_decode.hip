@@ -142,7 +142,8 @@ static_assert(sizeof(DecodePlan) == 1620, "MoePlan layout");
 // first appearances; its slot is the group's start plus the number of earlier entries with
 // the same expert. The groups' starts are a prefix sum of their sizes in first-appearance
 // order. An id outside [0, E) sets status bit 1 and leaves an empty plan (n_groups = 0).
-// The workgroup also copies the layer's validated address tables into their device snapshots.
+// The workgroup also copies the active experts' rows of the layer's validated address tables
+// into their device snapshots (the rest of a snapshot is never read through this plan).
 __global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) {
     __shared__ int32_t e_s[128];
     __shared__ uint32_t mask_s[2][2];
@@ -160,9 +161,6 @@ __global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) {
     e_s[tid] = e;
     __syncthreads();
     if (tid < n && (e < 0 || uint32_t(e) >= a.n_experts)) atomicOr(&bad_s, 1u);
-    // Snapshot copies (validated on the host into pinned ring slots).
-    for (uint32_t w = tid; w < a.snap_words; w += 128u) a.snap_dst[w] = a.snap_src[w];
-    for (uint32_t w = tid; w < a.snap_words2; w += 128u) a.snap_dst2[w] = a.snap_src2[w];
     __syncthreads();
     const bool bad = bad_s != 0u;
     uint32_t first = tid, rank = 0, size = 0;
@@ -208,6 +206,20 @@ __global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) {
     __syncthreads();
     uint32_t res_miss = 0;
     if (is_first) {
+        // The active expert's rows of both validated address tables (pinned ring slots), all
+        // six reads in flight together: the mat-vecs read no other rows of the snapshots.
+        const uint32_t r0 = 3u * uint32_t(e);
+        uint64_t v[6];
+#pragma unroll
+        for (uint32_t j = 0; j < 3u; ++j) {
+            v[j] = a.snap_words != 0u ? a.snap_src[r0 + j] : 0ull;
+            v[3 + j] = a.snap_words2 != 0u ? a.snap_src2[r0 + j] : 0ull;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 3u; ++j) {
+            if (a.snap_words != 0u) a.snap_dst[r0 + j] = v[j];
+            if (a.snap_words2 != 0u) a.snap_dst2[r0 + j] = v[3 + j];
+        }
         gidx_s[tid] = int32_t(gi);
         gstart_s[gi] = int32_t(start);
         const bool resident = a.resident == nullptr || a.resident[e] >= 0;
@@ -252,52 +264,58 @@ __device__ __forceinline__ Act load_act(const uint8_t* blk) {  // 36-byte blocks
     return a;
 }
 
-// Weight side of one 32-value block b of a row, per format: load() reads it once for every
-// entry; dot() returns the block's float contribution for one activation block.
-struct DotQ80 {  // 34 B / 32 values: d, int8 q[32] (blocks 2-byte aligned)
-    uint32_t w[8];
-    float d;
-    __device__ __forceinline__ void load(const uint8_t* row, uint32_t b) {
-        const uint8_t* p = row + 34u * b;
-        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-        const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-        // Nine dwords cover the block either way; the last may hold two bytes past the block
-        // (never past the page holding its last byte).
-        uint32_t v[9];
+// Weight side of a row, per format, in units that a lane takes whole: a Q4_K or Q2_K
+// super-block (256 values) or a pair of Q8_0 blocks (64 values). raw() issues the unit's
+// loads (kRaw dwords, every byte of the unit, nothing else); dot() takes sub-block s (32
+// values) of the loaded unit against one activation block.
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
+struct UnitQ80 {  // 2 x 34 B: d0, q0[32], d1, q1[32]; 4-byte aligned (rows hold whole pairs)
+    static constexpr uint32_t kVals = 64, kSub = 2, kRaw = 17;
+    __device__ __forceinline__ static void raw(const uint8_t* row, uint32_t u, uint32_t* r) {
+        const uint8_t* p = row + 68u * u;
 #pragma unroll
-        for (int i = 0; i < 9; ++i) v[i] = ld_global<uint32_t>(base + 4 * i);
-        // 4-aligned block: d at byte 0, codes at 2; otherwise d at byte 2, codes at 4.
-        const bool odd = (a & 3u) != 0u;
+        for (int i = 0; i < 4; ++i) {
+            const u32x4a v = ld_global<u32x4a>(p + 16 * i);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = odd ? v[i + 1] : __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
-        d = odd ? f16_hi(v[0]) : f16_lo(v[0]);
+            for (int j = 0; j < 4; ++j) r[4 * i + j] = v[j];
+        }
+        r[16] = ld_global<uint32_t>(p + 64);
     }
-    __device__ __forceinline__ float dot(const Act& x, float acc) const {
+    __device__ __forceinline__ static float dot(const uint32_t* r, uint32_t sb, const Act& x, float acc) {
+        // block 0: d in bytes 0-1, codes in bytes 2..33; block 1: d in bytes 34-35, codes 36..67
         int s = 0;
+        float d;
+        if (sb == 0u) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s = sdot4(w[i], x.q[i], s);
+            for (int i = 0; i < 8; ++i) s = sdot4(__builtin_amdgcn_alignbyte(r[i + 1], r[i], 2), x.q[i], s);
+            d = f16_lo(r[0]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = sdot4(r[9 + i], x.q[i], s);
+            d = f16_hi(r[8]);
+        }
         return __builtin_fmaf(d * x.d, float(s), acc);  // moe/native table: fma(d0 * d1, float(sumi), acc)
     }
 };
 
-struct DotQ4K {  // 144 B / 256 values: sub-block j (32 values) of the super-block per call
-    uint32_t w[8];
-    float d, dmin;
-    int sc, mn;
-    __device__ __forceinline__ void load(const uint8_t* row, uint32_t b) {
-        const uint8_t* sb = row + 144u * (b >> 3);
-        const uint32_t j = b & 7u, g = j >> 1, sh = 4u * (j & 1u);
-        const u32x4 hdr = ld_global<u32x4>(sb);
-        const u32x4 q0 = ld_global<u32x4>(sb + 16 + 32 * g), q1 = ld_global<u32x4>(sb + 32 + 32 * g);
+struct UnitQ4K {  // 144 B: d, dmin, scales[12], qs[128]; 16-byte aligned
+    static constexpr uint32_t kVals = 256, kSub = 8, kRaw = 36;
+    __device__ __forceinline__ static void raw(const uint8_t* row, uint32_t u, uint32_t* r) {
+        const uint8_t* p = row + 144u * u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w[i] = (q0[i] >> sh) & 0x0F0F0F0Fu;
-            w[4 + i] = (q1[i] >> sh) & 0x0F0F0F0Fu;
+        for (int i = 0; i < 9; ++i) {
+            const u32x4 v = ld_global<u32x4>(p + 16 * i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[4 * i + j] = v[j];
         }
-        d = f16_lo(hdr[0]);
-        dmin = f16_hi(hdr[0]);
-        // get_scale_min_k4 (dequant.hpp:157-190): scales bytes 0-11 are header bytes 4-15.
-        auto byte = [&](uint32_t k) { return (hdr[1 + k / 4] >> (8u * (k & 3u))) & 0xffu; };
+    }
+    __device__ __forceinline__ static float dot(const uint32_t* r, uint32_t j, const Act& x, float acc) {
+        // Sub-block j: the low (j even) or high nibbles of qs bytes 32 (j/2) .. +32, i.e. words
+        // 4 + 8 (j/2) .. +8; get_scale_min_k4 (dequant.hpp:157-190) over header bytes 4..15.
+        const uint32_t sh = 4u * (j & 1u), q0 = 4u + 8u * (j >> 1);
+        auto byte = [&](uint32_t k) { return (r[1 + k / 4] >> (8u * (k & 3u))) & 0xffu; };
+        int sc, mn;
         if (j < 4) {
             sc = int(byte(j) & 63u);
             mn = int(byte(j + 4) & 63u);
@@ -305,76 +323,80 @@ struct DotQ4K {  // 144 B / 256 values: sub-block j (32 values) of the super-blo
             sc = int((byte(j + 4) & 0xFu) | ((byte(j - 4) >> 6) << 4));
             mn = int((byte(j + 4) >> 4) | ((byte(j) >> 6) << 4));
         }
-    }
-    __device__ __forceinline__ float dot(const Act& x, float acc) const {
         int s = 0, t = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            s = sdot4(w[i], x.q[i], s);
+            s = sdot4((r[q0 + i] >> sh) & 0x0F0F0F0Fu, x.q[i], s);
             t = sdot4(0x01010101u, x.q[i], t);
         }
         const float sd = x.d * float(s * sc), sm = x.d * float(t * mn);
-        return acc + __builtin_fmaf(-dmin, sm, d * sd);  // q4_K: fma(-dm.y, sm, dm.x * sd), then acc + v
+        return acc + __builtin_fmaf(-f16_hi(r[0]), sm, f16_lo(r[0]) * sd);  // q4_K: fma(-dm.y, sm, dm.x * sd), then acc + v
     }
 };
 
-struct DotQ2K {  // 84 B / 256: scales[16] @0, q[64] @16, d @80, dmin @82
-    uint32_t w[8];
-    float d, dmin;
-    int sc0, mn0, sc1, mn1;
-    __device__ __forceinline__ void load(const uint8_t* row, uint32_t b) {
-        const uint8_t* sb = row + 84u * (b >> 3);
-        const uint32_t bb = b & 7u, nn = bb >> 2, j = bb & 3u;
-        // Values 128n + 32j + w (w < 32) use bits 2j of q[32n + w]; scale byte 8n + 2j + (w >= 16).
+struct UnitQ2K {  // 84 B: scales[16] @0, q[64] @16, d @80, dmin @82; 4-byte aligned
+    static constexpr uint32_t kVals = 256, kSub = 8, kRaw = 21;
+    __device__ __forceinline__ static void raw(const uint8_t* row, uint32_t u, uint32_t* r) {
+        const uint8_t* p = row + 84u * u;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = (ld_global<uint32_t>(sb + 16 + 32 * nn + 4 * i) >> (2u * j)) & 0x03030303u;
-        const uint32_t scw = ld_global<uint32_t>(sb + 8 * nn + 2 * (j & 2u));  // 4-aligned: bytes 8n + 4(j/2) ..
-        const uint32_t s0 = (scw >> (16u * (j & 1u))) & 0xffu, s1 = (scw >> (16u * (j & 1u) + 8u)) & 0xffu;
-        sc0 = int(s0 & 0xFu);
-        mn0 = int(s0 >> 4);
-        sc1 = int(s1 & 0xFu);
-        mn1 = int(s1 >> 4);
-        const uint32_t dd = ld_global<uint32_t>(sb + 80);
-        d = f16_lo(dd);
-        dmin = f16_hi(dd);
+        for (int i = 0; i < 5; ++i) {
+            const u32x4a v = ld_global<u32x4a>(p + 16 * i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[4 * i + j] = v[j];
+        }
+        r[20] = ld_global<uint32_t>(p + 80);
     }
-    __device__ __forceinline__ float dot(const Act& x, float acc) const {
-        int s0 = 0, s1 = 0, t0 = 0, t1 = 0;
+    __device__ __forceinline__ static float dot(const uint32_t* r, uint32_t bb, const Act& x, float acc) {
+        // Values 128n + 32j + w (w < 32) use bits 2j of q[32n + w]; scale byte 8n + 2j + (w >= 16).
+        const uint32_t nn = bb >> 2, j = bb & 3u;
+        const uint32_t scw = r[2 * nn + (j >> 1)];
+        const uint32_t s0 = (scw >> (16u * (j & 1u))) & 0xffu, s1 = (scw >> (16u * (j & 1u) + 8u)) & 0xffu;
+        int a0 = 0, a1 = 0, t0 = 0, t1 = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            s0 = sdot4(w[i], x.q[i], s0);
+            a0 = sdot4((r[4 + 8 * nn + i] >> (2u * j)) & 0x03030303u, x.q[i], a0);
             t0 = sdot4(0x01010101u, x.q[i], t0);
-            s1 = sdot4(w[4 + i], x.q[4 + i], s1);
+            a1 = sdot4((r[4 + 8 * nn + 4 + i] >> (2u * j)) & 0x03030303u, x.q[4 + i], a1);
             t1 = sdot4(0x01010101u, x.q[4 + i], t1);
         }
-        const float sd = x.d * float(s0 * sc0 + s1 * sc1), sm = x.d * float(t0 * mn0 + t1 * mn1);
-        return acc + __builtin_fmaf(-dmin, sm, d * sd);
+        const float sd = x.d * float(a0 * int(s0 & 0xFu) + a1 * int(s1 & 0xFu));
+        const float sm = x.d * float(t0 * int(s0 >> 4) + t1 * int(s1 >> 4));
+        return acc + __builtin_fmaf(-f16_hi(r[20]), sm, f16_lo(r[20]) * sd);
     }
 };
 
 // ---- grouped mat-vecs --------------------------------------------------------------------
-// Group g = blockIdx.y (blocks past n_groups exit); weight rows [32 * blockIdx.x, +32) of the
-// stage (gate/up: gate rows 0..I-1 then up rows I..2I-1; down: output rows 0..d-1), 8 per
-// wave. LPR lanes share a row (8..64, a power of two), each taking blocks lane % LPR + LPR * i
-// below K/32; the other lanes of the wave take the next rows. The launch picks the largest LPR
-// dividing K/32 so that every lane takes the same number of blocks; where no such LPR >= 8
-// exists (K = 640: 20 blocks) LPR is 8 and the last step leaves some lanes idle.
-constexpr uint32_t kRowsPerGroupBlock = 32;
+// Group g = blockIdx.y (blocks past n_groups exit). LPR lanes share a weight row (the
+// smallest power of two covering its units), each lane taking one whole unit, so a row's
+// bytes are all in flight at once and every byte loaded is used. A workgroup takes `iters`
+// consecutive slices of 4 * 64/LPR rows of the stage (gate/up: gate rows 0..I-1 then up rows
+// I..2I-1; down: output rows 0..d-1), one row per LPR-lane segment of a wave. The group's
+// activation blocks are staged in LDS once. Each lane keeps one accumulator per entry of the
+// group, a butterfly over the row's lanes finishes the row, and finished rows go to LDS; the
+// workgroup stores them after its last slice, consecutive lanes on consecutive columns (a
+// global store inside the loop would hold its registers until it completes).
 
+// A group holds at most one entry per token (a token's top-k experts are distinct), so at most
+// max_group = T entries: the LDS staging is sized for that.
 __device__ __forceinline__ bool plan_header_ok(const DecodePlan* P, uint32_t n_entries, uint32_t n_experts, uint32_t g,
-                                               uint32_t& a0, uint32_t& a1, uint32_t& ex) {
+                                               uint32_t max_group, uint32_t& a0, uint32_t& a1, uint32_t& ex) {
     if (P->n_entries != n_entries || P->n_groups == 0u || P->n_groups > 80u || g >= P->n_groups) return false;
     const int32_t s = P->grp_start[g], t = P->grp_start[g + 1], e = P->grp_e[g];
-    if (s < 0 || t <= s || uint32_t(t) > n_entries || uint32_t(t - s) > 8u || e < 0 || uint32_t(e) >= n_experts) return false;
+    if (s < 0 || t <= s || uint32_t(t) > n_entries || uint32_t(t - s) > max_group || e < 0 || uint32_t(e) >= n_experts)
+        return false;
     a0 = uint32_t(s);
     a1 = uint32_t(t);
     ex = uint32_t(e);
     return true;
 }
 
-template <class Dot, int MODE, uint32_t LPR>
-__global__ __launch_bounds__(256) void moe_matvec_kernel(DecodeMatvec m) {
-    constexpr uint32_t RPW = 64u / LPR;  // rows per wave pass
+__host__ __device__ constexpr uint32_t matvec_rows_per_block(uint32_t lpr) { return 4u * (64u / lpr); }
+
+template <class Unit, int MODE, uint32_t LPR>
+__global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  // >= 4 waves per SIMD
+    constexpr uint32_t RPW = 64u / LPR, RPI = 4u * RPW;  // rows per wave, rows per slice
+    // LDS: codes [entry][block] (8 words), then d [entry][block], then results [slice row][entry]
+    extern __shared__ uint32_t act_s[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t g = blockIdx.y;
     const DecodePlan* P = reinterpret_cast<const DecodePlan*>(m.plan);
@@ -394,7 +416,7 @@ __global__ __launch_bounds__(256) void moe_matvec_kernel(DecodeMatvec m) {
     }
     if (g >= P->n_groups) return;
     uint32_t a0, a1, ex;
-    if (!plan_header_ok(P, m.n_entries, m.n_experts, g, a0, a1, ex)) {
+    if (!plan_header_ok(P, m.n_entries, m.n_experts, g, m.max_group, a0, a1, ex)) {
         if (tid == 0 && blockIdx.x == 0u) atomicOr(m.status, 2u);
         return;  // the group's rows cannot be named: the whole stage's status reports it
     }
@@ -423,138 +445,206 @@ __global__ __launch_bounds__(256) void moe_matvec_kernel(DecodeMatvec m) {
     const uint8_t* w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
     const uint32_t fault = entries_ok ? weight_fault(w0, w1) : 2u;
     const uint32_t n_rows = MODE == kGateUp ? 2u * m.out_width : m.out_width;
-    const uint32_t nblk = m.k / 32u;
-    const uint32_t per_lane = (nblk + LPR - 1u) / LPR;
-    for (uint32_t it = 0; it < kRowsPerGroupBlock / (4u * RPW); ++it) {
-        const uint32_t row = kRowsPerGroupBlock * blockIdx.x + (it * 4u + wave) * RPW + lane / LPR;
-        const bool row_ok = row < n_rows;  // uniform within each LPR-lane segment
-        float acc[8];
-#pragma unroll
-        for (uint32_t c = 0; c < 8u; ++c) acc[c] = 0.0f;
-        if (row_ok && fault == 0u) {
-            const bool up = MODE == kGateUp && row >= m.out_width;
-            const uint8_t* wr = (up ? w1 : w0) + uint64_t(up ? row - m.out_width : row) * m.row_bytes;
-            for (uint32_t i = 0; i < per_lane; ++i) {
-                const uint32_t b = lane % LPR + LPR * i;  // the block of K this lane takes
-                if (b >= nblk) break;                     // ragged last step (K/32 not a multiple of LPR)
-                Dot wd;
-                wd.load(wr, b);
-#pragma unroll
-                for (uint32_t c = 0; c < 8u; ++c)
-                    if (c < n_e) acc[c] = wd.dot(load_act(m.act + (uint64_t(arow[c]) * nblk + b) * kQ81Bytes), acc[c]);
-            }
-        }
-        // Butterfly over the row's LPR lanes (xor LPR/2 .. 1).
-#pragma unroll
-        for (uint32_t c = 0; c < 8u; ++c)
-#pragma unroll
-            for (uint32_t o = LPR / 2u; o > 0u; o >>= 1) acc[c] = acc[c] + __shfl_xor(acc[c], int(o));
-        if (row_ok && lane % LPR == 0u) {
-            const bool up = MODE == kGateUp && row >= m.out_width;
+    const uint32_t rows_wg = m.iters * RPI, r_first = rows_wg * blockIdx.x;
+    if (fault != 0u) {
+        // The group's output rows of this workgroup are zeroed; the status reports the fault.
+        for (uint32_t i = r_first + tid; i < min(n_rows, r_first + rows_wg); i += 256u) {
+            const bool up = MODE == kGateUp && i >= m.out_width;
             float* out = up ? m.out1 : m.out0;
-            const uint32_t col = up ? row - m.out_width : row;
+            const uint32_t col = up ? i - m.out_width : i;
+            for (uint32_t c = 0; c < n_e; ++c) out[uint64_t(orow[c]) * m.out_width + col] = 0.0f;
+        }
+        if (tid == 0 && blockIdx.x == 0u) atomicOr(m.status, fault);
+        return;
+    }
+    const uint32_t nblk = m.k / 32u, nunit = m.k / Unit::kVals;
+    uint32_t* codes_s = act_s;                                               // [entry][block][8]
+    float* d_s = reinterpret_cast<float*>(act_s + m.max_group * nblk * 8u);  // [entry][block]
+    float* res_s = d_s + m.max_group * nblk;                                 // [slice row][entry]
+    // Stage the group's activation blocks: n_e rows of nblk Q8_1 blocks.
+    for (uint32_t i = tid; i < n_e * nblk * 9u; i += 256u) {
+        const uint32_t c = i / (nblk * 9u), rem = i - c * nblk * 9u, b = rem / 9u, w = rem - b * 9u;
+        const uint32_t v = ld_global<uint32_t>(m.act + (uint64_t(arow[c]) * nblk + b) * kQ81Bytes + 4u * w);
+        if (w == 0u) d_s[c * nblk + b] = f16_lo(v);
+        else codes_s[(c * nblk + b) * 8u + (w - 1u)] = v;
+    }
+    __syncthreads();
+    const uint32_t seg = lane % LPR;
+    const bool unit_ok = seg < nunit;
+    const uint32_t u = unit_ok ? seg : nunit - 1u;
+    for (uint32_t it = 0; it < m.iters; ++it) {
+        const uint32_t lr = it * RPI + wave * RPW + lane / LPR, row = r_first + lr;
+        const uint32_t rowc = row < n_rows ? row : n_rows - 1u;
+        const bool up = MODE == kGateUp && rowc >= m.out_width;
+        const uint8_t* wr = (up ? w1 : w0) + uint64_t(up ? rowc - m.out_width : rowc) * m.row_bytes;
+        uint32_t r[Unit::kRaw];
+        Unit::raw(wr, u, r);
+        // One entry at a time (n_e is uniform over the workgroup): the unit's sub-blocks against
+        // the entry's activation blocks, then the butterfly over the row's LPR lanes.
+        for (uint32_t c = 0; c < n_e; ++c) {
+            // Opaque to the optimiser, so the codes are decoded per entry instead of all eight
+            // sub-blocks being decoded once and held (64 more registers).
 #pragma unroll
-            for (uint32_t c = 0; c < 8u; ++c)
-                if (c < n_e) out[uint64_t(orow[c]) * m.out_width + col] = fault == 0u ? acc[c] : 0.0f;
+            for (uint32_t i = 0; i < Unit::kRaw; ++i) __asm__ volatile("" : "+v"(r[i]));
+            float acc = 0.0f;
+            if (unit_ok) {
+#pragma unroll
+                for (uint32_t sb = 0; sb < Unit::kSub; ++sb) {
+                    const uint32_t b = u * Unit::kSub + sb;
+                    const uint32_t* cs = codes_s + (c * nblk + b) * 8u;
+                    const u32x4 qa = *reinterpret_cast<const u32x4*>(cs), qb = *reinterpret_cast<const u32x4*>(cs + 4);
+                    Act a;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        a.q[i] = qa[i];
+                        a.q[4 + i] = qb[i];
+                    }
+                    a.d = d_s[c * nblk + b];
+                    acc = Unit::dot(r, sb, a, acc);
+                    // The next pair's LDS reads stay below this pair's dots (register budget).
+                    if (sb & 1u) __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (uint32_t o = LPR / 2u; o > 0u; o >>= 1) acc = acc + __shfl_xor(acc, int(o));
+            if (seg == 0u) res_s[lr * m.max_group + c] = acc;
         }
     }
-    if (fault != 0u && tid == 0 && blockIdx.x == 0u) atomicOr(m.status, fault);
+    __syncthreads();  // every slice's rows are in LDS
+    for (uint32_t i = tid; i < rows_wg * n_e; i += 256u) {
+        const uint32_t c = i / rows_wg, lr = i - c * rows_wg, row = r_first + lr;
+        if (row >= n_rows) continue;
+        const bool up = MODE == kGateUp && row >= m.out_width;
+        float* out = up ? m.out1 : m.out0;
+        const uint32_t col = up ? row - m.out_width : row;
+        out[uint64_t(orow[c]) * m.out_width + col] = res_s[lr * m.max_group + c];
+    }
 }
 
-// ---- the shared expert: dense mat-vecs over F16 / BF16 weights ---------------------------
-// Rows [32 * blockIdx.x, +32) of the output, 8 per wave; LPR lanes share a weight row, each
-// taking 8-value chunks lane % LPR + LPR * i (one 16-byte load of the weight row). Every lane
-// keeps one accumulator per activation row (two in gate/up: the gate and up rows of the same
-// output column), and a butterfly over the row's lanes finishes them. gate/up applies the
-// F32 SwiGLU silu(g) * u before its one store (the reference's shx_swiglu, moe.metal:237-245).
-template <bool BF, bool GATE_UP, uint32_t LPR>
+// ---- dense mat-vecs: the shared expert (F16 / BF16 weights) and the router (F32 weights) --
+// 4 * 64/LPR output rows per workgroup, one per LPR-lane segment of a wave; the row's lanes
+// take 16-byte weight chunks lane % LPR + LPR * i (8 F16/BF16 values or 4 F32 values), up to
+// kPerLane at once before using any, and keep one accumulator per activation row (two in
+// gate/up: the gate and up rows of the same output column); a butterfly finishes each row.
+// gate/up applies the F32 SwiGLU silu(g) * u before its one store (the reference's shx
+// SwiGLU, moe.metal:243-251); the router adds the bias after the dot.
+enum { kWF16 = 0, kWBF16 = 1, kWF32 = 2 };
+constexpr uint32_t kPerLane = 4;
+
+template <int WT, bool GATE_UP, bool XF32, uint32_t LPR>
 __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
     constexpr uint32_t RPW = 64u / LPR;
     constexpr uint32_t NW = GATE_UP ? 2u : 1u;
+    constexpr uint32_t VPC = WT == kWF32 ? 4u : 8u;  // values per 16-byte chunk
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t nch = m.k / 8u;
+    const uint32_t nch = m.k / VPC;
     const uint32_t per_lane = (nch + LPR - 1u) / LPR;
-    for (uint32_t it = 0; it < kRowsPerGroupBlock / (4u * RPW); ++it) {
-        const uint32_t row = kRowsPerGroupBlock * blockIdx.x + (it * 4u + wave) * RPW + lane / LPR;
-        const bool row_ok = row < m.n_out;  // uniform within each LPR-lane segment
-        float acc[NW][8];
+    const uint32_t row = matvec_rows_per_block(LPR) * blockIdx.x + wave * RPW + lane / LPR;
+    const bool row_ok = row < m.n_out;  // uniform within each LPR-lane segment
+    const uint32_t wbytes = WT == kWF32 ? 4u : 2u;
+    float acc[NW][8];
 #pragma unroll
-        for (uint32_t w = 0; w < NW; ++w)
+    for (uint32_t w = 0; w < NW; ++w)
 #pragma unroll
-            for (uint32_t t = 0; t < 8u; ++t) acc[w][t] = 0.0f;
-        if (row_ok) {
-            const uint8_t* wr[2] = {m.w0 + uint64_t(row) * m.k * 2u, GATE_UP ? m.w1 + uint64_t(row) * m.k * 2u : nullptr};
-            for (uint32_t i = 0; i < per_lane; ++i) {
-                const uint32_t c = lane % LPR + LPR * i;
-                if (c >= nch) break;
-                float wv[NW][8];
+        for (uint32_t t = 0; t < 8u; ++t) acc[w][t] = 0.0f;
+    if (row_ok) {
+        const uint8_t* wr[2] = {m.w0 + uint64_t(row) * m.k * wbytes,
+                                GATE_UP ? m.w1 + uint64_t(row) * m.k * wbytes : nullptr};
+        for (uint32_t base = 0; base < per_lane; base += kPerLane) {
+            u32x4 raw[NW][kPerLane];
 #pragma unroll
-                for (uint32_t w = 0; w < NW; ++w) {
-                    const u32x4 q = ld_global<u32x4>(wr[w] + 16u * c);
+            for (uint32_t i = 0; i < kPerLane; ++i) {
+                const uint32_t c = lane % LPR + LPR * (base + i);
+                if (c < nch)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        if (BF) {
-                            wv[w][2 * j] = bits_f32(q[j] << 16);
-                            wv[w][2 * j + 1] = bits_f32(q[j] & 0xffff0000u);
+                    for (uint32_t w = 0; w < NW; ++w) raw[w][i] = ld_global<u32x4>(wr[w] + 16u * c);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < kPerLane; ++i) {
+                const uint32_t c = lane % LPR + LPR * (base + i);
+                if (c >= nch) continue;
+                float wv[NW][VPC];
+#pragma unroll
+                for (uint32_t w = 0; w < NW; ++w)
+#pragma unroll
+                    for (uint32_t j = 0; j < 4u; ++j) {
+                        const uint32_t q = raw[w][i][j];
+                        if (WT == kWF32) {
+                            wv[w][j] = bits_f32(q);
+                        } else if (WT == kWBF16) {
+                            wv[w][2 * j] = bits_f32(q << 16);
+                            wv[w][2 * j + 1] = bits_f32(q & 0xffff0000u);
                         } else {
-                            wv[w][2 * j] = f16_lo(q[j]);
-                            wv[w][2 * j + 1] = f16_hi(q[j]);
+                            wv[w][2 * j] = f16_lo(q);
+                            wv[w][2 * j + 1] = f16_hi(q);
                         }
                     }
-                }
 #pragma unroll
                 for (uint32_t t = 0; t < 8u; ++t) {
                     if (t >= m.rows) break;
-                    float xv[8];
-                    if (GATE_UP) {
-                        const u32x4 q = ld_global<u32x4>(reinterpret_cast<const uint8_t*>(m.x) + (uint64_t(t) * m.k + 8u * c) * 2u);
+                    float xv[VPC];
+                    if (XF32) {
+                        const float* xp = reinterpret_cast<const float*>(m.x) + uint64_t(t) * m.k + VPC * c;
+                        const float4v a = ld_global<float4v>(xp);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            xv[2 * j] = f16_lo(q[j]);
-                            xv[2 * j + 1] = f16_hi(q[j]);
+                        for (uint32_t j = 0; j < 4u; ++j) xv[j] = a[j];
+                        if (VPC == 8u) {
+                            const float4v b = ld_global<float4v>(xp + 4);
+#pragma unroll
+                            for (uint32_t j = 0; j < 4u; ++j) xv[(4u + j) % VPC] = b[j];
                         }
                     } else {
-                        const float* xp = reinterpret_cast<const float*>(m.x) + uint64_t(t) * m.k + 8u * c;
-                        const float4v a = ld_global<float4v>(xp), b = ld_global<float4v>(xp + 4);
+                        const uint8_t* xp = reinterpret_cast<const uint8_t*>(m.x) + (uint64_t(t) * m.k + VPC * c) * 2u;
+                        if (VPC == 8u) {
+                            const u32x4 q = ld_global<u32x4>(xp);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            xv[j] = a[j];
-                            xv[4 + j] = b[j];
+                            for (uint32_t j = 0; j < 4u; ++j) {
+                                xv[(2u * j) % VPC] = f16_lo(q[j]);
+                                xv[(2u * j + 1u) % VPC] = f16_hi(q[j]);
+                            }
+                        } else {
+                            const uint32_t q0 = ld_global<uint32_t>(xp), q1 = ld_global<uint32_t>(xp + 4);
+                            xv[0] = f16_lo(q0);
+                            xv[1] = f16_hi(q0);
+                            xv[2 % VPC] = f16_lo(q1);
+                            xv[3 % VPC] = f16_hi(q1);
                         }
                     }
 #pragma unroll
                     for (uint32_t w = 0; w < NW; ++w)
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) acc[w][t] = __builtin_fmaf(wv[w][j], xv[j], acc[w][t]);
+                        for (uint32_t j = 0; j < VPC; ++j) acc[w][t] = __builtin_fmaf(wv[w][j], xv[j], acc[w][t]);
                 }
             }
         }
+    }
 #pragma unroll
-        for (uint32_t w = 0; w < NW; ++w)
+    for (uint32_t w = 0; w < NW; ++w)
 #pragma unroll
-            for (uint32_t t = 0; t < 8u; ++t)
+        for (uint32_t t = 0; t < 8u; ++t)
+            if (t < m.rows)
 #pragma unroll
                 for (uint32_t o = LPR / 2u; o > 0u; o >>= 1) acc[w][t] = acc[w][t] + __shfl_xor(acc[w][t], int(o));
-        if (row_ok && lane % LPR == 0u) {
+    if (row_ok && lane % LPR == 0u) {
+        const float b = (!GATE_UP && m.bias != nullptr) ? m.bias[row] : 0.0f;
 #pragma unroll
-            for (uint32_t t = 0; t < 8u; ++t)
-                if (t < m.rows)
-                    m.out[uint64_t(t) * m.n_out + row] = GATE_UP ? silu(acc[0][t]) * acc[NW - 1][t] : acc[0][t];
-        }
+        for (uint32_t t = 0; t < 8u; ++t)
+            if (t < m.rows)
+                m.out[uint64_t(t) * m.n_out + row] = GATE_UP ? silu(acc[0][t]) * acc[NW - 1][t] : acc[0][t] + b;
     }
 }
 
-template <bool BF, bool GATE_UP>
+template <int WT, bool GATE_UP, bool XF32>
 hipError_t launch_dense_decode_t(const DenseDecode& m, hipStream_t s) {
-    const uint32_t nch = m.k / 8u;
-    uint32_t lpr = 64;
-    while (lpr > 8u && nch % lpr != 0u) lpr >>= 1;
-    const dim3 grid((m.n_out + kRowsPerGroupBlock - 1) / kRowsPerGroupBlock);
+    const uint32_t nch = m.k / (WT == kWF32 ? 4u : 8u);
+    uint32_t lpr = 8;
+    while (lpr < 64u && (nch + lpr - 1u) / lpr > kPerLane) lpr <<= 1;
+    const dim3 grid((m.n_out + matvec_rows_per_block(lpr) - 1u) / matvec_rows_per_block(lpr));
     switch (lpr) {
-        case 64: dense_decode_kernel<BF, GATE_UP, 64><<<grid, 256, 0, s>>>(m); break;
-        case 32: dense_decode_kernel<BF, GATE_UP, 32><<<grid, 256, 0, s>>>(m); break;
-        case 16: dense_decode_kernel<BF, GATE_UP, 16><<<grid, 256, 0, s>>>(m); break;
-        default: dense_decode_kernel<BF, GATE_UP, 8><<<grid, 256, 0, s>>>(m); break;
+        case 64: dense_decode_kernel<WT, GATE_UP, XF32, 64><<<grid, 256, 0, s>>>(m); break;
+        case 32: dense_decode_kernel<WT, GATE_UP, XF32, 32><<<grid, 256, 0, s>>>(m); break;
+        case 16: dense_decode_kernel<WT, GATE_UP, XF32, 16><<<grid, 256, 0, s>>>(m); break;
+        default: dense_decode_kernel<WT, GATE_UP, XF32, 8><<<grid, 256, 0, s>>>(m); break;
     }
     return hipGetLastError();
 }
@@ -592,19 +682,29 @@ __global__ __launch_bounds__(256) void snapshot_copy_kernel(const uint64_t* src,
     if (threadIdx.x == 0 && status != nullptr) *status = 0u;
 }
 
-template <class Dot, int MODE>
-hipError_t launch_matvec_t(const DecodeMatvec& m, hipStream_t s) {
+template <class Unit, int MODE>
+hipError_t launch_matvec_t(const DecodeMatvec& mm, hipStream_t s) {
+    DecodeMatvec m = mm;
     const uint32_t n_rows = MODE == kGateUp ? 2u * m.out_width : m.out_width;
-    const dim3 grid((n_rows + kRowsPerGroupBlock - 1) / kRowsPerGroupBlock, 80);
-    const uint32_t nblk = m.k / 32u;
-    if (nblk == 0u) return hipErrorInvalidValue;
-    uint32_t lpr = 64;
-    while (lpr > 8u && nblk % lpr != 0u) lpr >>= 1;
+    const uint32_t nblk = m.k / 32u, nunit = m.k / Unit::kVals;
+    if (nunit == 0u || nunit > 64u || m.k % Unit::kVals != 0u) return hipErrorInvalidValue;  // host-checked
+    if (m.max_group == 0u || m.max_group > 8u) return hipErrorInvalidValue;
+    uint32_t lpr = 1;
+    while (lpr < nunit) lpr <<= 1;
+    if (lpr < 8u) lpr = 8u;
+    // Slices per workgroup: up to 4 once the groups (at most one per routed entry) give the
+    // chip about four workgroups per CU without them; one when there are few groups (T = 1).
+    const uint32_t rpi = matvec_rows_per_block(lpr);
+    const uint32_t slices = (n_rows + rpi - 1u) / rpi;
+    const uint32_t per_iter = m.n_entries * slices;  // workgroups at one slice each (upper bound)
+    m.iters = per_iter >= 4096u ? 4u : per_iter >= 2048u ? 2u : 1u;
+    const dim3 grid((slices + m.iters - 1u) / m.iters, 80);
+    const size_t lds = size_t(m.max_group) * nblk * 9u * 4u + size_t(m.iters) * rpi * m.max_group * 4u;
     switch (lpr) {
-        case 64: moe_matvec_kernel<Dot, MODE, 64><<<grid, 256, 0, s>>>(m); break;
-        case 32: moe_matvec_kernel<Dot, MODE, 32><<<grid, 256, 0, s>>>(m); break;
-        case 16: moe_matvec_kernel<Dot, MODE, 16><<<grid, 256, 0, s>>>(m); break;
-        default: moe_matvec_kernel<Dot, MODE, 8><<<grid, 256, 0, s>>>(m); break;
+        case 64: moe_matvec_kernel<Unit, MODE, 64><<<grid, 256, lds, s>>>(m); break;
+        case 32: moe_matvec_kernel<Unit, MODE, 32><<<grid, 256, lds, s>>>(m); break;
+        case 16: moe_matvec_kernel<Unit, MODE, 16><<<grid, 256, lds, s>>>(m); break;
+        default: moe_matvec_kernel<Unit, MODE, 8><<<grid, 256, lds, s>>>(m); break;
     }
     return hipGetLastError();
 }
@@ -630,20 +730,36 @@ hipError_t launch_quantize_q8_1(const void* x, bool f32_input, uint8_t* y, uint3
 
 hipError_t launch_decode_matvec(Fmt fmt, bool gate_up, const DecodeMatvec& m, hipStream_t s) {
     switch (fmt) {
-        case Fmt::Q8_0: return gate_up ? launch_matvec_t<DotQ80, kGateUp>(m, s) : launch_matvec_t<DotQ80, kDown>(m, s);
-        case Fmt::Q4_K: return gate_up ? launch_matvec_t<DotQ4K, kGateUp>(m, s) : launch_matvec_t<DotQ4K, kDown>(m, s);
-        case Fmt::Q2_K: return gate_up ? launch_matvec_t<DotQ2K, kGateUp>(m, s) : launch_matvec_t<DotQ2K, kDown>(m, s);
+        case Fmt::Q8_0: return gate_up ? launch_matvec_t<UnitQ80, kGateUp>(m, s) : launch_matvec_t<UnitQ80, kDown>(m, s);
+        case Fmt::Q4_K: return gate_up ? launch_matvec_t<UnitQ4K, kGateUp>(m, s) : launch_matvec_t<UnitQ4K, kDown>(m, s);
+        case Fmt::Q2_K: return gate_up ? launch_matvec_t<UnitQ2K, kGateUp>(m, s) : launch_matvec_t<UnitQ2K, kDown>(m, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipStream_t s) {
     if (m.rows == 0u || m.rows > 8u || m.k == 0u || m.k % 64u != 0u) return hipErrorInvalidValue;
-    switch (fmt) {
-        case Fmt::F16: return gate_up ? launch_dense_decode_t<false, true>(m, s) : launch_dense_decode_t<false, false>(m, s);
-        case Fmt::BF16: return gate_up ? launch_dense_decode_t<true, true>(m, s) : launch_dense_decode_t<true, false>(m, s);
+    switch (fmt) {  // gate/up reads the F16 mixed activation; down the F32 hidden
+        case Fmt::F16:
+            return gate_up ? launch_dense_decode_t<kWF16, true, false>(m, s) : launch_dense_decode_t<kWF16, false, true>(m, s);
+        case Fmt::BF16:
+            return gate_up ? launch_dense_decode_t<kWBF16, true, false>(m, s) : launch_dense_decode_t<kWBF16, false, true>(m, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
+                                uint32_t d, uint32_t E, hipStream_t s) {
+    if (rows == 0u || rows > 8u || d == 0u || d % 64u != 0u) return hipErrorInvalidValue;
+    DenseDecode m{};
+    m.w0 = reinterpret_cast<const uint8_t*>(w);
+    m.x = x;
+    m.bias = bias;
+    m.out = logits;
+    m.rows = rows;
+    m.k = d;
+    m.n_out = E;
+    return launch_dense_decode_t<kWF32, false, false>(m, s);
 }
 
 hipError_t launch_swiglu_f32(const float* gate, const float* up, float* out, uint64_t n, hipStream_t s) {

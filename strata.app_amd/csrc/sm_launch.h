@@ -193,6 +193,8 @@ struct DecodeMatvec {
     uint32_t n_entries, n_experts, act_rows;
     uint32_t k, out_width;
     uint64_t row_bytes;
+    uint32_t max_group;  // entries a group may hold (T: one per token); larger groups are a bad plan
+    uint32_t iters;      // set by the launcher: row slices per workgroup
 };
 hipError_t launch_decode_matvec(Fmt fmt, bool gate_up, const DecodeMatvec& m, hipStream_t s);
 hipError_t launch_swiglu_f32(const float* gate, const float* up, float* out, uint64_t n, hipStream_t s);
@@ -203,10 +205,15 @@ struct DenseDecode {
     const uint8_t* w0;
     const uint8_t* w1;
     const void* x;
+    const float* bias;  // router only (may be null)
     float* out;
     uint32_t rows, k, n_out;
 };
 hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipStream_t s);
+// The router of a decode layer (T <= 8 rows): logits[t][e] = x_t . W_e + bias[e] with F32
+// weights [E][d] and F32 accumulation (d a multiple of 64).
+hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
+                                uint32_t d, uint32_t E, hipStream_t s);
 // out = (p_0 w_0 + sum_r fma) + shared * sigmoid(gl); shared == null: no shared term.
 hipError_t launch_combine_decode(const float* parts, const float* w, const float* shared, const float* gl, float* out,
                                  uint32_t rows, uint32_t top_k, uint32_t d, hipStream_t s);

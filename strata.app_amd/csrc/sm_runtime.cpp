@@ -1520,6 +1520,10 @@ sm_status decode_shape_check(const sm_moe_shape* s, const char* prefix, std::str
         err = std::string(prefix) + " requires T=1..8 rows and at most 80 routed entries";
         return SM_E_SHAPE;
     }
+    if (s->hidden > SM_DECODE_MAX_WIDTH || (need_ff && s->expert_ff > SM_DECODE_MAX_WIDTH)) {
+        err = std::string(prefix) + " widths above 4096 are not supported";
+        return SM_E_SHAPE;
+    }
     return SM_OK;
 }
 
@@ -1588,6 +1592,7 @@ sm::DecodeMatvec decode_matvec(const sm_moe_shape& s, int fmt, bool gate_up, con
     m.k = gate_up ? s.hidden : s.expert_ff;
     m.out_width = gate_up ? s.expert_ff : s.hidden;
     m.row_bytes = fmt_row_bytes(fmt, m.k);
+    m.max_group = s.rows;
     return m;
 }
 
@@ -1928,10 +1933,10 @@ sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape,
         return ring_fail(seg, claim_status(s_dn));
     }
     const auto rows = s.rows, d = s.hidden, E = s.n_experts;
-    add_step(seg, "router GEMM", [=](hipStream_t st2) {
-        return sm::launch_router_gemm(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
-                                      reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits), rows,
-                                      d, E, st2);
+    add_step(seg, "decode router", [=](hipStream_t st2) {
+        return sm::launch_router_decode(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
+                                        reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits), rows,
+                                        d, E, st2);
     });
     encode_route_launch(seg, s, 0, ro);  // multiply mode (the Window's route)
     sm::DecodePlanArgs pa = decode_plan_args(s, pr);
