@@ -410,8 +410,8 @@ sm_status sm_encode_moe_routed_ffn(sm_segment* seg, const sm_moe_shape* shape, s
 /* encode_moe_combine — moe_dispatch.hpp:277-280 (the decode combine: the first rank a product,
  * the others fma, the gated shared output added last; moe.metal:253-274). */
 sm_status sm_encode_moe_combine(sm_segment* seg, const sm_moe_shape* shape, const sm_combine_buffers* b);
-/* encode_moe_shared_ffn — moe_dispatch.hpp:287-308: shared gate/up + F32 SwiGLU, down, the
- * sigmoid gate logit, then the decode combine (4 launches). */
+/* encode_moe_shared_ffn — moe_dispatch.hpp:287-308: shared gate/up + F32 SwiGLU (with the
+ * sigmoid gate logit in the same launch), down, then the decode combine (3 launches). */
 sm_status sm_encode_moe_shared_ffn(sm_segment* seg, const sm_moe_shape* shape, sm_format fmt,
                                    const sm_moe_shared_ffn_buffers* b);
 /* The Window MoE FFN of one layer (moe_dispatch.hpp:339-372's composition, with the route and

@@ -89,19 +89,11 @@ __device__ int q81_round_subnormal_input(uint32_t value_bits, uint32_t d_bits) {
     return (value_bits & 0x80000000u) ? -m : m;
 }
 
-// One thread per value, 32 lanes per block (n is a multiple of 32, so each 32-lane half of a
-// wave exits or stays as a whole). amax is reduced over the absolute bit patterns and the
-// sum over the unrounded values, both with xor 16, 8, 4, 2, 1 butterflies.
-template <bool F32IN>
-__global__ __launch_bounds__(256) void q8_1_kernel(const void* x, uint8_t* y, uint32_t n, uint32_t rows) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x, r = blockIdx.y;
-    if (r >= rows || i >= n) return;
-    uint32_t vb;
-    if (F32IN) {
-        vb = reinterpret_cast<const uint32_t*>(x)[uint64_t(r) * n + i];
-    } else {
-        vb = f32_bits(float(reinterpret_cast<const _Float16*>(x)[uint64_t(r) * n + i]));
-    }
+// Quantizes value i of a row (its F32 bits vb) into the row's Q8_1 blocks y; all 32 lanes of
+// the value's block call it together (lanes 32 apart hold the same position of two blocks).
+// amax is reduced over the absolute bit patterns and the sum over the unrounded values, both
+// with xor 16, 8, 4, 2, 1 butterflies.
+__device__ __forceinline__ void q8_1_value(uint32_t vb, uint8_t* y, uint32_t i) {
     const float xi = bits_f32(vb);
     uint32_t amax = vb & 0x7fffffffu;
     float sum = xi;
@@ -121,12 +113,36 @@ __global__ __launch_bounds__(256) void q8_1_kernel(const void* x, uint8_t* y, ui
     else if (de == 0u) q = q81_round_subnormal_division(vb, d_bits);
     else if (ve == 0u) q = q81_round_subnormal_input(vb, d_bits);
     else q = round_away(__fdiv_rn(xi, d));
-    uint8_t* blk = y + (uint64_t(r) * (n / 32u) + i / 32u) * kQ81Bytes;
+    uint8_t* blk = y + uint64_t(i / 32u) * kQ81Bytes;
     blk[4 + (i & 31u)] = uint8_t(int8_t(q));
     if ((i & 31u) == 0u) {
         const uint32_t ds = uint32_t(f16_bits(_Float16(d))) | (uint32_t(f16_bits(_Float16(sum))) << 16);
         *reinterpret_cast<uint32_t*>(blk) = ds;
     }
+}
+
+// One thread per value (n is a multiple of 32, so each 32-lane half of a wave exits or stays
+// as a whole).
+template <bool F32IN>
+__global__ __launch_bounds__(256) void q8_1_kernel(const void* x, uint8_t* y, uint32_t n, uint32_t rows) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x, r = blockIdx.y;
+    if (r >= rows || i >= n) return;
+    const uint32_t vb = F32IN ? reinterpret_cast<const uint32_t*>(x)[uint64_t(r) * n + i]
+                              : f32_bits(float(reinterpret_cast<const _Float16*>(x)[uint64_t(r) * n + i]));
+    q8_1_value(vb, y + uint64_t(r) * (n / 32u) * kQ81Bytes, i);
+}
+
+// The decode SwiGLU fused with the Q8_1 quantization of its output: hidden = silu(g) * u in F32
+// (moe.metal:213-221), stored, and quantized for the down mat-vec. One thread per value of a
+// rows x n array (n a multiple of 32).
+__global__ __launch_bounds__(256) void swiglu_q8_1_kernel(const float* gate, const float* up, float* hidden, uint8_t* y,
+                                                          uint32_t n, uint32_t rows) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x, r = blockIdx.y;
+    if (r >= rows || i >= n) return;
+    const uint64_t at = uint64_t(r) * n + i;
+    const float h = silu(gate[at]) * up[at];
+    hidden[at] = h;
+    q8_1_value(f32_bits(h), y + uint64_t(r) * (n / 32u) * kQ81Bytes, i);
 }
 
 // ---- the plan ----------------------------------------------------------------------------
@@ -142,9 +158,7 @@ static_assert(sizeof(DecodePlan) == 1620, "MoePlan layout");
 // first appearances; its slot is the group's start plus the number of earlier entries with
 // the same expert. The groups' starts are a prefix sum of their sizes in first-appearance
 // order. An id outside [0, E) sets status bit 1 and leaves an empty plan (n_groups = 0).
-// The workgroup also copies the active experts' rows of the layer's validated address tables
-// into their device snapshots (the rest of a snapshot is never read through this plan).
-__global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) {
+__device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
     __shared__ int32_t e_s[128];
     __shared__ uint32_t mask_s[2][2];
     __shared__ uint32_t size_w[2];
@@ -206,20 +220,6 @@ __global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) {
     __syncthreads();
     uint32_t res_miss = 0;
     if (is_first) {
-        // The active expert's rows of both validated address tables (pinned ring slots), all
-        // six reads in flight together: the mat-vecs read no other rows of the snapshots.
-        const uint32_t r0 = 3u * uint32_t(e);
-        uint64_t v[6];
-#pragma unroll
-        for (uint32_t j = 0; j < 3u; ++j) {
-            v[j] = a.snap_words != 0u ? a.snap_src[r0 + j] : 0ull;
-            v[3 + j] = a.snap_words2 != 0u ? a.snap_src2[r0 + j] : 0ull;
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < 3u; ++j) {
-            if (a.snap_words != 0u) a.snap_dst[r0 + j] = v[j];
-            if (a.snap_words2 != 0u) a.snap_dst2[r0 + j] = v[3 + j];
-        }
         gidx_s[tid] = int32_t(gi);
         gstart_s[gi] = int32_t(start);
         const bool resident = a.resident == nullptr || a.resident[e] >= 0;
@@ -244,6 +244,20 @@ __global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) {
         // Tiered mode: one use per entry (exact in F32 below 2^24).
         if (a.usage != nullptr) atomicAdd(&a.usage[e], 1.0f);
     }
+}
+
+__global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) { moe_plan_body(a); }
+
+// The plan (workgroup 0, 128 threads) and the Q8_1 quantization of the layer's F16 input rows
+// (the other workgroups, 128 values each) in one launch: neither reads what the other writes.
+__global__ __launch_bounds__(128) void plan_q8_1_kernel(DecodePlanArgs a, const _Float16* x, uint8_t* y, uint32_t n) {
+    if (blockIdx.x == 0) {
+        moe_plan_body(a);
+        return;
+    }
+    const uint32_t per_row = n / 128u, b = blockIdx.x - 1u;
+    const uint32_t r = b / per_row, i = (b - r * per_row) * 128u + threadIdx.x;
+    q8_1_value(f32_bits(float(x[uint64_t(r) * n + i])), y + uint64_t(r) * (n / 32u) * kQ81Bytes, i);
 }
 
 // ---- block dots over Q8_1 ----------------------------------------------------------------
@@ -531,8 +545,49 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
 enum { kWF16 = 0, kWBF16 = 1, kWF32 = 2 };
 constexpr uint32_t kPerLane = 4;
 
+// The shared expert's sigmoid-gate logits gl[t] = x_t . gv (one workgroup: wave w takes
+// tokens w and w + 4; each lane 8 consecutive values per 16-byte load into two partial sums,
+// then a fixed xor butterfly).
+template <int WT>
+__device__ __forceinline__ void gate_logit_block(const DenseDecode& m) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const _Float16* x = reinterpret_cast<const _Float16*>(m.x);
+    for (uint32_t t = wave; t < m.rows; t += 4u) {
+        float s0 = 0.0f, s1 = 0.0f;
+        for (uint32_t k = 8u * lane; k < m.k; k += 512u) {
+            const half8 xv = ld_global<half8>(x + uint64_t(t) * m.k + k);
+            const u32x4 wv = ld_global<u32x4>(m.gv + 2u * k);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t pair = wv[i];
+                const float w0 = WT == kWBF16 ? bits_f32(pair << 16) : f16_lo(pair);
+                const float w1 = WT == kWBF16 ? bits_f32(pair & 0xffff0000u) : f16_hi(pair);
+                s0 = __builtin_fmaf(float(xv[2 * i]), w0, s0);
+                s1 = __builtin_fmaf(float(xv[2 * i + 1]), w1, s1);
+            }
+        }
+        float sum = s0 + s1;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off);
+        if (lane == 0) m.gl[t] = sum;
+    }
+}
+
 template <int WT, bool GATE_UP, bool XF32, uint32_t LPR>
 __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
+    if (GATE_UP && m.gv != nullptr && blockIdx.x == gridDim.x - 1u) {
+        gate_logit_block<WT>(m);  // the launch's last workgroup
+        return;
+    }
+    if (!GATE_UP && blockIdx.x >= m.row_blocks) {
+        // The router launch's extra workgroups: one 8-byte word each per thread of the
+        // validated address tables (pinned ring slots) into their device snapshots, read once
+        // across PCIe beside the router's own work.
+        const uint32_t w = (blockIdx.x - m.row_blocks) * 256u + threadIdx.x;
+        if (w < m.snap_words) m.snap_dst[w] = m.snap_src[w];
+        else if (w - m.snap_words < m.snap_words2) m.snap_dst2[w - m.snap_words] = m.snap_src2[w - m.snap_words];
+        return;
+    }
     constexpr uint32_t RPW = 64u / LPR;
     constexpr uint32_t NW = GATE_UP ? 2u : 1u;
     constexpr uint32_t VPC = WT == kWF32 ? 4u : 8u;  // values per 16-byte chunk
@@ -639,12 +694,16 @@ hipError_t launch_dense_decode_t(const DenseDecode& m, hipStream_t s) {
     const uint32_t nch = m.k / (WT == kWF32 ? 4u : 8u);
     uint32_t lpr = 8;
     while (lpr < 64u && (nch + lpr - 1u) / lpr > kPerLane) lpr <<= 1;
-    const dim3 grid((m.n_out + matvec_rows_per_block(lpr) - 1u) / matvec_rows_per_block(lpr));
+    DenseDecode mm = m;
+    mm.row_blocks = (m.n_out + matvec_rows_per_block(lpr) - 1u) / matvec_rows_per_block(lpr);
+    // Extra workgroups: the gate logit (shared gate/up) or the snapshot copies (router).
+    const uint32_t extra = GATE_UP ? (m.gv != nullptr ? 1u : 0u) : (m.snap_words + m.snap_words2 + 255u) / 256u;
+    const dim3 grid(mm.row_blocks + extra);
     switch (lpr) {
-        case 64: dense_decode_kernel<WT, GATE_UP, XF32, 64><<<grid, 256, 0, s>>>(m); break;
-        case 32: dense_decode_kernel<WT, GATE_UP, XF32, 32><<<grid, 256, 0, s>>>(m); break;
-        case 16: dense_decode_kernel<WT, GATE_UP, XF32, 16><<<grid, 256, 0, s>>>(m); break;
-        default: dense_decode_kernel<WT, GATE_UP, XF32, 8><<<grid, 256, 0, s>>>(m); break;
+        case 64: dense_decode_kernel<WT, GATE_UP, XF32, 64><<<grid, 256, 0, s>>>(mm); break;
+        case 32: dense_decode_kernel<WT, GATE_UP, XF32, 32><<<grid, 256, 0, s>>>(mm); break;
+        case 16: dense_decode_kernel<WT, GATE_UP, XF32, 16><<<grid, 256, 0, s>>>(mm); break;
+        default: dense_decode_kernel<WT, GATE_UP, XF32, 8><<<grid, 256, 0, s>>>(mm); break;
     }
     return hipGetLastError();
 }
@@ -716,6 +775,20 @@ hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t launch_decode_plan_q8_1(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
+                                   hipStream_t s) {
+    if (n == 0u || n % 128u != 0u) return hipErrorInvalidValue;
+    plan_q8_1_kernel<<<1u + rows * (n / 128u), 128, 0, s>>>(a, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_q8_1(const float* gate, const float* up, float* hidden, uint8_t* y, uint32_t n, uint32_t rows,
+                              hipStream_t s) {
+    if (n == 0u || n % 32u != 0u) return hipErrorInvalidValue;
+    swiglu_q8_1_kernel<<<dim3((n + 255u) / 256u, rows), 256, 0, s>>>(gate, up, hidden, y, n, rows);
+    return hipGetLastError();
+}
+
 hipError_t launch_snapshot_copy(const uint64_t* src, uint64_t* dst, uint32_t words, uint32_t* status, hipStream_t s) {
     snapshot_copy_kernel<<<1, 256, 0, s>>>(src, dst, words, status);
     return hipGetLastError();
@@ -749,9 +822,15 @@ hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipS
 }
 
 hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
-                                uint32_t d, uint32_t E, hipStream_t s) {
+                                uint32_t d, uint32_t E, const SnapshotCopy& snap, hipStream_t s) {
     if (rows == 0u || rows > 8u || d == 0u || d % 64u != 0u) return hipErrorInvalidValue;
     DenseDecode m{};
+    m.snap_src = snap.src;
+    m.snap_dst = snap.dst;
+    m.snap_words = snap.words;
+    m.snap_src2 = snap.src2;
+    m.snap_dst2 = snap.dst2;
+    m.snap_words2 = snap.words2;
     m.w0 = reinterpret_cast<const uint8_t*>(w);
     m.x = x;
     m.bias = bias;

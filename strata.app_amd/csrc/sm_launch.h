@@ -168,14 +168,14 @@ struct DecodePlanArgs {
     uint8_t* plan;              // the layer's MoePlan
     uint32_t* status;           // bit 1 on an id outside [0, E) (may be null)
     uint32_t rows, top_k, n_experts;
-    const uint64_t* snap_src;
-    uint64_t* snap_dst;
-    uint32_t snap_words;
-    const uint64_t* snap_src2;
-    uint64_t* snap_dst2;
-    uint32_t snap_words2;
 };
 hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t s);
+// The plan and the Q8_1 quantization of rows x n F16 input values (n a multiple of 128), one launch.
+hipError_t launch_decode_plan_q8_1(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
+                                   hipStream_t s);
+// hidden = silu(gate) * up (F32, rows x n, n a multiple of 32) and its Q8_1 blocks y, one launch.
+hipError_t launch_swiglu_q8_1(const float* gate, const float* up, float* hidden, uint8_t* y, uint32_t n, uint32_t rows,
+                              hipStream_t s);
 // A standalone expert stage's snapshot copy (src may be null: nothing copied); clears *status.
 hipError_t launch_snapshot_copy(const uint64_t* src, uint64_t* dst, uint32_t words, uint32_t* status, hipStream_t s);
 // Q8_1 blocks (36 B: half d, half sum, int8 q[32]) of rows x n values (F16 or F32 input).
@@ -208,12 +208,31 @@ struct DenseDecode {
     const float* bias;  // router only (may be null)
     float* out;
     uint32_t rows, k, n_out;
+    const uint8_t* gv;  // gate/up only: the sigmoid-gate vector [k] (may be null) ...
+    float* gl;          // ... and its logits [rows], computed by one more workgroup of the launch
+    // router only: address tables to copy into their snapshots (words may be 0)
+    const uint64_t* snap_src;
+    uint64_t* snap_dst;
+    uint32_t snap_words;
+    const uint64_t* snap_src2;
+    uint64_t* snap_dst2;
+    uint32_t snap_words2;
+    uint32_t row_blocks;  // set by the launcher
+};
+struct SnapshotCopy {
+    const uint64_t* src;
+    uint64_t* dst;
+    uint32_t words;
+    const uint64_t* src2;
+    uint64_t* dst2;
+    uint32_t words2;
 };
 hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipStream_t s);
 // The router of a decode layer (T <= 8 rows): logits[t][e] = x_t . W_e + bias[e] with F32
 // weights [E][d] and F32 accumulation (d a multiple of 64).
+// The launch also copies the validated address tables of `snap` into their device snapshots.
 hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
-                                uint32_t d, uint32_t E, hipStream_t s);
+                                uint32_t d, uint32_t E, const SnapshotCopy& snap, hipStream_t s);
 // out = (p_0 w_0 + sum_r fma) + shared * sigmoid(gl); shared == null: no shared term.
 hipError_t launch_combine_decode(const float* parts, const float* w, const float* shared, const float* gl, float* out,
                                  uint32_t rows, uint32_t top_k, uint32_t d, hipStream_t s);

@@ -1690,6 +1690,8 @@ void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt
     gu.rows = s.rows;
     gu.k = s.hidden;
     gu.n_out = s.shared_ff;
+    gu.gv = reinterpret_cast<const uint8_t*>(r.gv);
+    gu.gl = reinterpret_cast<float*>(r.gl);
     sm::DenseDecode dn{};
     dn.w0 = reinterpret_cast<const uint8_t*>(r.wd);
     dn.x = reinterpret_cast<const void*>(r.hidden);
@@ -1697,14 +1699,8 @@ void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt
     dn.rows = s.rows;
     dn.k = s.shared_ff;
     dn.n_out = s.hidden;
-    const auto rows = s.rows, d = s.hidden;
-    const uintptr_t x = r.x, gv = r.gv, gl = r.gl;
     add_step(seg, "decode shared gate/up", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), true, gu, st); });
     add_step(seg, "decode shared down", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), false, dn, st); });
-    add_step(seg, "shared gate logit", [=](hipStream_t st) {
-        return sm::launch_gate_logit(Fmt(fmt), reinterpret_cast<const _Float16*>(x), reinterpret_cast<const uint8_t*>(gv),
-                                     reinterpret_cast<float*>(gl), rows, d, st);
-    });
 }
 
 // The routed FFN's scratch and output views (gate, up, hidden, Q8_1 hidden, parts, status).
@@ -1737,8 +1733,12 @@ sm_status encode_routed_ffn_launch(sm_segment* seg, const sm_moe_shape& s, int f
         const sm_status st = encode_decode_stage(seg, s, fgu, true, r.gu, true);
         if (st != SM_OK) return st;
     }
-    encode_swiglu_f32_launch(seg, r.gu.out0, r.gu.out1, r.hidden, N * s.expert_ff);
-    encode_q81_launch(seg, r.hidden, true, r.hq, s.expert_ff, uint32_t(N), "decode Q8_1 hidden");
+    const uintptr_t g = r.gu.out0, u = r.gu.out1, h = r.hidden, hq = r.hq;
+    const uint32_t I = s.expert_ff, rows = uint32_t(N);
+    add_step(seg, "decode swiglu + Q8_1", [=](hipStream_t st) {
+        return sm::launch_swiglu_q8_1(reinterpret_cast<const float*>(g), reinterpret_cast<const float*>(u),
+                                      reinterpret_cast<float*>(h), reinterpret_cast<uint8_t*>(hq), I, rows, st);
+    });
     if (snapshots_done) {
         const sm::DecodeMatvec m = decode_matvec(s, fdn, false, r.dn);
         add_step(seg, "decode down", [=](hipStream_t st) { return sm::launch_decode_matvec(Fmt(fdn), false, m, st); });
@@ -1933,23 +1933,28 @@ sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape,
         return ring_fail(seg, claim_status(s_dn));
     }
     const auto rows = s.rows, d = s.hidden, E = s.n_experts;
+    // The router launch copies both validated address tables; the plan reads no table.
+    sm::SnapshotCopy snap{};
+    snap.src = s_gu >= 0 ? seg->ctx->ring + uint64_t(s_gu) * sm_context::kSlotWords : nullptr;
+    snap.dst = reinterpret_cast<uint64_t*>(fr.gu.w.snapshot);
+    snap.words = s_gu >= 0 ? uint32_t(fr.gu.w.table.size()) : 0u;
+    snap.src2 = s_dn >= 0 ? seg->ctx->ring + uint64_t(s_dn) * sm_context::kSlotWords : nullptr;
+    snap.dst2 = reinterpret_cast<uint64_t*>(fr.dn.w.snapshot);
+    snap.words2 = s_dn >= 0 ? uint32_t(fr.dn.w.table.size()) : 0u;
     add_step(seg, "decode router", [=](hipStream_t st2) {
         return sm::launch_router_decode(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
                                         reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits), rows,
-                                        d, E, st2);
+                                        d, E, snap, st2);
     });
-    encode_route_launch(seg, s, 0, ro);  // multiply mode (the Window's route)
-    sm::DecodePlanArgs pa = decode_plan_args(s, pr);
-    pa.snap_src = s_gu >= 0 ? seg->ctx->ring + uint64_t(s_gu) * sm_context::kSlotWords : nullptr;
-    pa.snap_dst = reinterpret_cast<uint64_t*>(fr.gu.w.snapshot);
-    pa.snap_words = s_gu >= 0 ? uint32_t(fr.gu.w.table.size()) : 0u;
-    pa.snap_src2 = s_dn >= 0 ? seg->ctx->ring + uint64_t(s_dn) * sm_context::kSlotWords : nullptr;
-    pa.snap_dst2 = reinterpret_cast<uint64_t*>(fr.dn.w.snapshot);
-    pa.snap_words2 = s_dn >= 0 ? uint32_t(fr.dn.w.table.size()) : 0u;
-    add_step(seg, "decode plan", [=](hipStream_t st2) { return sm::launch_decode_plan(pa, st2); });
     seg->steps.back().ring_slot = s_gu;
     seg->steps.back().ring_slot2 = s_dn;
-    encode_q81_launch(seg, rr.x, false, xq, s.hidden, s.rows, "decode Q8_1 input");
+    encode_route_launch(seg, s, 0, ro);  // multiply mode (the Window's route)
+    const sm::DecodePlanArgs pa = decode_plan_args(s, pr);
+    const uintptr_t x = rr.x;
+    add_step(seg, "decode plan + Q8_1 input", [=](hipStream_t st2) {
+        return sm::launch_decode_plan_q8_1(pa, reinterpret_cast<const _Float16*>(x), reinterpret_cast<uint8_t*>(xq), d,
+                                           rows, st2);
+    });
     if ((st = encode_routed_ffn_launch(seg, s, f->gate_up, f->down, fr, true)) != SM_OK) return st;
     if (s.shared_ff != 0) encode_shared_decode_launch(seg, s, f->shared, sr);
     encode_combine_decode_launch(seg, s, cr);

@@ -104,23 +104,23 @@ def test_decode_coordinators_encode(moe, fd):
     assert fd.run(lambda s: s.encode_moe_down(fd.shape, moe.Q8_0, db))[::2] == (True, 2)
     sb = moe.SwiGLUBuffers(fd.gate.view(), fd.up.view(), fd.hidden.view())
     assert fd.run(lambda s: s.encode_moe_swiglu(40, 256, sb))[::2] == (True, 1)
-    # snapshot, gate/up, SwiGLU, Q8_1, snapshot, down
-    assert fd.run(lambda s: s.encode_moe_routed_ffn(fd.shape, moe.Q4_K, moe.Q8_0, fd.routed()))[::2] == (True, 6)
+    # snapshot, gate/up, SwiGLU + Q8_1, snapshot, down
+    assert fd.run(lambda s: s.encode_moe_routed_ffn(fd.shape, moe.Q4_K, moe.Q8_0, fd.routed()))[::2] == (True, 5)
     cb = moe.CombineBuffers(fd.parts.view(), fd.rw.view(), fd.sh_o.view(), fd.sh_gl.view(), fd.out.view())
     assert fd.run(lambda s: s.encode_moe_combine(fd.shape, cb))[::2] == (True, 1)
-    # shared gate/up + SwiGLU, down, gate logit, combine
+    # shared gate/up + SwiGLU (+ the gate logit), down, combine
     sfb = moe.MoeSharedFFNBuffers(fd.layer_buffers().shared, fd.parts.view(), fd.rw.view(), fd.out.view())
-    assert fd.run(lambda s: s.encode_moe_shared_ffn(fd.shape, moe.F16, sfb))[::2] == (True, 4)
+    assert fd.run(lambda s: s.encode_moe_shared_ffn(fd.shape, moe.F16, sfb))[::2] == (True, 3)
     sfb.shared.hidden = fd.sh_h.view(0, fd.shape.rows * fd.shape.shared_ff * 2)  # an F16-sized hidden
     ok, err, _ = fd.run(lambda s: s.encode_moe_shared_ffn(fd.shape, moe.F16, sfb))
     assert not ok and "shared hidden view is undersized" in err
-    # router, top-k, plan, Q8_1, gate/up, SwiGLU, Q8_1, down, shared x3, combine
+    # router, top-k, plan + Q8_1, gate/up, SwiGLU + Q8_1, down, shared x2, combine
     ok, err, n = fd.run(lambda s: s.encode_moe_decode_layer(fd.shape, fd.fmts, fd.layer_buffers()))
     assert ok, err
-    assert n == 12
+    assert n == 9
     ns = shape_with(moe, fd.shape, shared_ff=0)
     ok, err, n = fd.run(lambda s: s.encode_moe_decode_layer(ns, fd.fmts, fd.layer_buffers()))
-    assert ok and n == 9, err
+    assert ok and n == 7, err
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -186,6 +186,6 @@ def test_decode_reference_model_widths(moe):
     of that width are rejected."""
     fd = FakeDecode(moe, T=8, d=2560, E=64, K=10, I=640, Is=640, fmt_gu=2, fmt_dn=1)
     ok, err, n = fd.run(lambda s: s.encode_moe_decode_layer(fd.shape, fd.fmts, fd.layer_buffers()))
-    assert ok and n == 12, err
+    assert ok and n == 9, err
     ok, err, _ = fd.run(lambda s: s.encode_moe_routed_ffn(fd.shape, moe.Q4_K, moe.Q4_K, fd.routed()))
     assert not ok and "expert weight extent is invalid" in err
