@@ -391,18 +391,7 @@ struct UnitQ2K {  // 84 B: scales[16] @0, q[64] @16, d @80, dmin @82; 4-byte ali
 // global store inside the loop would hold its registers until it completes).
 
 // A group holds at most one entry per token (a token's top-k experts are distinct), so at most
-// max_group = T entries: the LDS staging is sized for that.
-__device__ __forceinline__ bool plan_header_ok(const DecodePlan* P, uint32_t n_entries, uint32_t n_experts, uint32_t g,
-                                               uint32_t max_group, uint32_t& a0, uint32_t& a1, uint32_t& ex) {
-    if (P->n_entries != n_entries || P->n_groups == 0u || P->n_groups > 80u || g >= P->n_groups) return false;
-    const int32_t s = P->grp_start[g], t = P->grp_start[g + 1], e = P->grp_e[g];
-    if (s < 0 || t <= s || uint32_t(t) > n_entries || uint32_t(t - s) > max_group || e < 0 || uint32_t(e) >= n_experts)
-        return false;
-    a0 = uint32_t(s);
-    a1 = uint32_t(t);
-    ex = uint32_t(e);
-    return true;
-}
+// max_group = T entries: the LDS staging is sized for that, and a larger group is a bad plan.
 
 __host__ __device__ constexpr uint32_t matvec_rows_per_block(uint32_t lpr) { return 4u * (64u / lpr); }
 
@@ -417,7 +406,10 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
     if (g >= 80u) return;
     // A plan whose header is unusable: workgroup (0, 0) reports it and zeroes every output row
     // this stage could have written.
-    const bool plan_ok = P->n_entries == m.n_entries && P->n_groups <= 80u;
+    // Every plan field this workgroup needs, read in one round trip (g < 80: all inside the plan).
+    const uint32_t p_entries = P->n_entries, p_groups = P->n_groups;
+    const int32_t p_s = P->grp_start[g], p_t = P->grp_start[g + 1], p_e = P->grp_e[g];
+    const bool plan_ok = p_entries == m.n_entries && p_groups <= 80u;
     if (!plan_ok) {
         if (g != 0u || blockIdx.x != 0u) return;
         if (tid == 0) atomicOr(m.status, 2u);
@@ -428,12 +420,13 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
                 for (uint64_t i = tid; i < total; i += 256u) outs[o][i] = 0.0f;
         return;
     }
-    if (g >= P->n_groups) return;
-    uint32_t a0, a1, ex;
-    if (!plan_header_ok(P, m.n_entries, m.n_experts, g, m.max_group, a0, a1, ex)) {
+    if (g >= p_groups) return;
+    if (p_groups == 0u || p_s < 0 || p_t <= p_s || uint32_t(p_t) > m.n_entries || uint32_t(p_t - p_s) > m.max_group ||
+        p_e < 0 || uint32_t(p_e) >= m.n_experts) {
         if (tid == 0 && blockIdx.x == 0u) atomicOr(m.status, 2u);
         return;  // the group's rows cannot be named: the whole stage's status reports it
     }
+    const uint32_t a0 = uint32_t(p_s), a1 = uint32_t(p_t), ex = uint32_t(p_e);
     const uint32_t n_e = a1 - a0;
     // Entries: activation row (gate/up: the token; down: the grouped entry) and output row
     // (gate/up: the grouped entry; down: the route index from ent_dst).
@@ -472,6 +465,15 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
         return;
     }
     const uint32_t nblk = m.k / 32u, nunit = m.k / Unit::kVals;
+    const uint32_t seg = lane % LPR;
+    const bool unit_ok = seg < nunit;
+    const uint32_t u = unit_ok ? seg : nunit - 1u;
+    auto row_ptr = [&](uint32_t it) {  // this lane's row of slice it (clamped into the stage)
+        const uint32_t row = r_first + it * RPI + wave * RPW + lane / LPR;
+        const uint32_t rowc = row < n_rows ? row : n_rows - 1u;
+        const bool up = MODE == kGateUp && rowc >= m.out_width;
+        return (up ? w1 : w0) + uint64_t(up ? rowc - m.out_width : rowc) * m.row_bytes;
+    };
     uint32_t* codes_s = act_s;                                               // [entry][block][8]
     float* d_s = reinterpret_cast<float*>(act_s + m.max_group * nblk * 8u);  // [entry][block]
     float* res_s = d_s + m.max_group * nblk;                                 // [slice row][entry]
@@ -483,16 +485,10 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
         else codes_s[(c * nblk + b) * 8u + (w - 1u)] = v;
     }
     __syncthreads();
-    const uint32_t seg = lane % LPR;
-    const bool unit_ok = seg < nunit;
-    const uint32_t u = unit_ok ? seg : nunit - 1u;
     for (uint32_t it = 0; it < m.iters; ++it) {
-        const uint32_t lr = it * RPI + wave * RPW + lane / LPR, row = r_first + lr;
-        const uint32_t rowc = row < n_rows ? row : n_rows - 1u;
-        const bool up = MODE == kGateUp && rowc >= m.out_width;
-        const uint8_t* wr = (up ? w1 : w0) + uint64_t(up ? rowc - m.out_width : rowc) * m.row_bytes;
+        const uint32_t lr = it * RPI + wave * RPW + lane / LPR;
         uint32_t r[Unit::kRaw];
-        Unit::raw(wr, u, r);
+        Unit::raw(row_ptr(it), u, r);
         // One entry at a time (n_e is uniform over the workgroup): the unit's sub-blocks against
         // the entry's activation blocks, then the butterfly over the row's LPR lanes.
         for (uint32_t c = 0; c < n_e; ++c) {
