@@ -30,9 +30,18 @@ constexpr int kSlab = 256;  // values per K slab (one Q4_K / Q2_K super-block, e
 // ---------------------------------------------------------------------------------------
 constexpr int kV2Threads = 512;
 
-// Position (in 16-byte chunks) of chunk c of row r inside a swizzled 64 x 256 slab: the
-// 16 rows one MFMA A-fragment read touches map to 16 distinct 4-bank groups.
-__device__ __forceinline__ uint32_t a_pos(uint32_t r, uint32_t c) { return r * 32u + (c ^ (r & 15u)); }
+// Position (in 16-byte chunks) of chunk c of row r inside a swizzled 64 x 256 slab. LDS has
+// 64 banks of 4 bytes, so a 16-byte chunk at position p sits in bank group p % 16, and a
+// ds_read_b128 of 64 lanes is served in passes of 16 lanes that never pair two lanes with the
+// same lane % 16 (a plain linear read is conflict-free) but do pair lanes of different
+// 16-lane quarters. An A-fragment read (lane n + 16 gq: row 16 rb + n, chunk 8 gq + s) must
+// therefore put every lane in a bank group that depends on n alone: here n ^ s. Positions
+// are grouped as [rb][gq][n & 7][16], so each 16-chunk group holds chunks 8 gq .. 8 gq + 7 of
+// rows n and n + 8 (two whole 128-byte lines of the activation rows).
+__device__ __forceinline__ uint32_t a_pos(uint32_t r, uint32_t c) {
+    const uint32_t n = r & 15u;
+    return 16u * (32u * (r >> 4) + 8u * (c >> 3) + (n & 7u)) + (n ^ (c & 7u));
+}
 
 template <int MODE>
 __device__ void zero_cols(const RoutedGemm& g, uint32_t r0, uint32_t r1, uint32_t c0, uint32_t c1, bool by_dst) {
@@ -129,14 +138,17 @@ __device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_
 }
 
 // Activation copy map of one 64 x 256 slab: wave instruction q = 4*wave + j (j = 0..3)
-// fills chunk positions [64q, 64q + 64): row R = 2q + lane/32, swizzled chunk
-// C = (lane & 31) ^ (R & 15). Rows past the tile's end repeat its last row.
+// fills chunk positions [64q, 64q + 64), the inverse of a_pos: position 16 Q + rho holds
+// row 16 (Q >> 5) + ((Q & 7) | (rho & 8)), chunk 8 ((Q >> 3) & 3) + ((rho & 7) ^ (Q & 7)).
+// Each instruction reads eight whole 128-byte lines (8 rows x 8 chunks). Rows past the
+// tile's end repeat its last row.
 __device__ __forceinline__ void slab_sources(const RoutedGemm& g, const TileWork& t, int wave, int lane,
                                              const _Float16* (&asrc)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t R = 2u * (4u * wave + j) + (uint32_t(lane) >> 5);
-        const uint32_t C = (uint32_t(lane) & 31u) ^ (R & 15u);
+        const uint32_t Q = 4u * (4u * wave + j) + (uint32_t(lane) >> 4), rho = uint32_t(lane) & 15u;
+        const uint32_t R = 16u * (Q >> 5) + ((Q & 7u) | (rho & 8u));
+        const uint32_t C = 8u * ((Q >> 3) & 3u) + ((rho & 7u) ^ (Q & 7u));
         uint32_t row = t.a0 + R;
         if (row > t.a1 - 1u) row = t.a1 - 1u;
         asrc[j] = g.a + uint64_t(row) * g.k + 8u * C;
