@@ -427,49 +427,98 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
         for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
     constexpr bool DIRECT = DirectWeights<Frag, MODE, RESIDENT>::value;
     if constexpr (DIRECT) {
-        // This lane's fragments of `step`, from global memory.
-        auto load_frags = [&](Frag (&c)[NF], uint32_t step) {
-            const uint32_t nt = t.nt_begin + step / n_slabs, sb = step % n_slabs;
+        // Steps are (column tile, half f): the wave's 16 weight rows of fragment f, rows
+        // 128 f + 16 wave + n of the column tile, with every slab of them loaded at once, so a
+        // step's eight waves read 128 consecutive rows whole. The 128-byte lines that two slabs
+        // of a row share, and the end of one row with the start of the next (rows are 4.25
+        // lines), are then fetched by one step, where loads a step apart fetched some of them
+        // twice (lines evicted in between). The column tile's F32 results go out through LDS
+        // (the weight image is unused here), so `parts` rows are written as whole 1 KB pieces.
+        auto load_step = [&](auto& c, uint32_t tile, int f) {
+            const uint32_t r = (t.nt_begin + tile) * S::kImageRows + 128u * uint32_t(f) + 16u * uint32_t(wave) + uint32_t(n);
 #pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                const uint32_t r = nt * S::kImageRows + S::image_row(wave, n, f);
-                c[f].template load<FromGlobal>(t.w0 + uint64_t(r) * g.row_bytes + uint64_t(sb) * SB, gq);
+            for (int sb = 0; sb < int(sizeof(c) / sizeof(c[0])); ++sb)
+                c[sb][0].template load<FromGlobal>(t.w0 + uint64_t(r) * g.row_bytes + uint64_t(sb) * SB, gq);
+        };
+        // The finished column tile: accumulators -> LDS [row][256 + 4 pad] (the pad puts the
+        // four lane groups' rows in distinct banks), then each wave stores 8 rows, 64 lanes x 16
+        // bytes per row. Rows past the tile's end are not stored; a destination outside [0, N)
+        // is reported (status bit 1) and the entry's own row is zeroed instead.
+        constexpr uint32_t kStageRow = 260u;
+        static_assert(64u * kStageRow * 4u <= StagedBuffers<Frag, NF>::kImage, "output tile must fit the image buffer");
+        float* stage = reinterpret_cast<float*>(sw[0]);
+        auto epilogue = [&](auto rb_const, float4v (&acc)[2][1][4], uint32_t tile) {
+            constexpr int RB = decltype(rb_const)::value;
+            __syncthreads();  // the previous tile's rows have been read out
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t row = 16u * rb + 4u * gq + i, col = 128u * f + 16u * wave + n;
+                        stage[row * kStageRow + col] = acc[f][0][rb][i];
+                        acc[f][0][rb][i] = 0.0f;
+                    }
+            __syncthreads();
+            const uint32_t col0 = (t.nt_begin + tile) * S::kOut;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t row = 8u * wave + j, a = t.a0 + row;
+                if (row >= 16u * RB || a >= t.a1) continue;  // wave-uniform
+                const uint32_t d = s_dst[row];
+                const bool good = d < g.n_entries;
+                if (!good && lane == 0) atomicOr(g.status, 2u);
+                float4v v = *reinterpret_cast<const float4v*>(stage + row * kStageRow + 4u * lane);
+                if (!good) v = float4v{0, 0, 0, 0};
+                // Write-once rows: non-temporal, so they do not evict the weight lines that the
+                // next step of this or another item still reads.
+                __builtin_nontemporal_store(v, reinterpret_cast<float4v*>(g.out_f + uint64_t(good ? d : a) * g.n_out + col0 + 4u * lane));
             }
         };
-        auto run_direct = [&](auto rb_const) {
+        auto run_direct = [&](auto rb_const, auto ns_const) {
             constexpr int RB = decltype(rb_const)::value;
-            float4v acc[NF][4];
+            constexpr int NS = decltype(ns_const)::value;  // slabs (K = 256 NS)
+            float4v acc[2][1][4];
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
+            for (int f = 0; f < 2; ++f)
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
-            Frag fa[NF], fb[NF];
-            load_frags(fa, 0);
-            // Steps in pairs, so the two fragment sets alternate without copies.
-            auto do_step = [&](uint32_t step, Frag (&cur)[NF], Frag (&nxt)[NF]) {
-                // The resident slabs (first step) and this step's fragments.
-                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                if (step == 0) __syncthreads();
-                load_frags(nxt, step + 1 < n_steps ? step + 1 : step);
+                for (int rb = 0; rb < 4; ++rb) acc[f][0][rb] = float4v{0, 0, 0, 0};
+            const uint32_t n_tiles = t.nt_end - t.nt_begin;
+            Frag fa[NS][1], fb[NS][1];
+            load_step(fa, 0, 0);
+            auto do_step = [&](Frag (&cur)[NS][1], float4v (&acc_f)[1][4]) {
 #pragma unroll
-                for (int f = 0; f < NF; ++f) cur[f].prepare();
-                const uint32_t sb = step % n_slabs;
-                slab_mma<Frag, NF, RB>(sa[sb], n, gq, cur, acc, [](int) {});
-                if (sb == n_slabs - 1u)
-                    staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, (t.nt_begin + step / n_slabs) * S::kOut, wave, n,
-                                                  gq, acc);
+                for (int sb = 0; sb < NS; ++sb) {
+                    cur[sb][0].prepare();
+                    slab_mma<Frag, 1, RB>(sa[sb], n, gq, cur[sb], acc_f, [](int) {});
+                }
             };
-            for (uint32_t step = 0; step < n_steps; step += 2) {
-                do_step(step, fa, fb);
-                if (step + 1 < n_steps) do_step(step + 1, fb, fa);
+            for (uint32_t tile = 0; tile < n_tiles; ++tile) {
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // fa: (tile, f = 0)
+                if (tile == 0) __syncthreads();                         // the resident slabs
+                load_step(fb, tile, 1);
+                // The loads stay ahead of this step's work (left alone, the scheduler sinks them
+                // below the multiplies, and the next step then waits for their whole latency).
+                __builtin_amdgcn_sched_barrier(0);
+                do_step(fa, acc[0]);
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // fb: (tile, f = 1)
+                load_step(fa, tile + 1 < n_tiles ? tile + 1 : tile, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                do_step(fb, acc[1]);
+                epilogue(rb_const, acc, tile);
             }
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated last fragment loads
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated last loads
+        };
+        auto run_ns = [&](auto rb_const) {
+            if (n_slabs == 2u) run_direct(rb_const, std::integral_constant<int, 2>());
+            else run_direct(rb_const, std::integral_constant<int, 1>());
         };
         switch ((t.a1 - t.a0 + 15u) / 16u) {  // workgroup-uniform
-            case 1: run_direct(std::integral_constant<int, 1>()); break;
-            case 2: run_direct(std::integral_constant<int, 2>()); break;
-            case 3: run_direct(std::integral_constant<int, 3>()); break;
-            default: run_direct(std::integral_constant<int, 4>()); break;
+            case 1: run_ns(std::integral_constant<int, 1>()); break;
+            case 2: run_ns(std::integral_constant<int, 2>()); break;
+            case 3: run_ns(std::integral_constant<int, 3>()); break;
+            default: run_ns(std::integral_constant<int, 4>()); break;
         }
         if (dynamic && threadIdx.x == 0) sm.s_next = x * per + next;
         continue;
