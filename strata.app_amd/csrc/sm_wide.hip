@@ -19,9 +19,10 @@
 //   down:    output columns [64q, +64).
 // Each 16-value K slice's operands are read from LDS while the previous slice multiplies.
 // The two waves of a SIMD (w and w + 4) take different row halves.
-// Items are spread XCD-aware: unit u runs on XCD u % 8 (workgroup b runs on XCD b % 8) and
-// the column tiles of a unit are neighbours in that XCD's item order, so they run together
-// and share the unit's activation rows in that XCD's L2.
+// Items are spread XCD-aware: XCD x (workgroup b runs on XCD b % 8) takes a contiguous eighth
+// of the units, so the units of one expert share its weight rows in one L2, and the column
+// tiles of a unit are neighbours in that XCD's item order, so they run together and share the
+// unit's activation rows.
 #include <type_traits>
 
 #include "sm_device.h"
@@ -307,11 +308,15 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
     const uint32_t prow = tid >> 1, pb = tid & 1u;  // producer: B row and byte half
 
     const uint32_t x = blockIdx.x & 7u, l = blockIdx.x >> 3, P = gridDim.x >> 3;
-    const uint32_t vx = U > x ? (U - x + 7u) >> 3 : 0u;
+    // XCD x takes the contiguous unit range [x U / 8, (x + 1) U / 8): the units of one expert
+    // (consecutive unit indices) then share its weight rows in one XCD's L2 instead of every
+    // XCD reading the whole expert.
+    const uint32_t u_begin = uint32_t((uint64_t(x) * U) >> 3), u_end = uint32_t((uint64_t(x + 1u) * U) >> 3);
+    const uint32_t vx = u_end - u_begin;
     const uint32_t n_items = vx * n_ct;
     const uint32_t nK = g.k / kStepK;
     for (uint32_t m = l; m < n_items; m += P) {
-        const uint32_t v = m / n_ct, ct = m - v * n_ct, uidx = x + 8u * v;
+        const uint32_t v = m / n_ct, ct = m - v * n_ct, uidx = u_begin + v;
         Unit u;
         if (DENSE) {
             u.a0 = kUnitRows * uidx;
