@@ -170,12 +170,15 @@ struct FragQ4K {
         const uint32_t sc_hi = (h1 & mh) | ((a1 >> sa) & ma);
         const uint32_t mn_hi = ((h1 >> 4) & mh) | ((m1 >> sa) & ma);
         d_lo = d * float(sc_lo); m_lo = -(dmin * float(mn_lo));
-        d_hi = d * float(sc_hi); m_hi = -(dmin * float(mn_hi));
+        // The high nibbles are converted in place (q & 0xF0, i.e. 16 * nibble) and scaled by
+        // d_hi / 16, exact in F32 (d_hi >= 2^-24), so fma(d_hi / 16, 16 q, m_hi) is the same
+        // single rounding of d_hi * q + m_hi and the shift per dword is saved.
+        d_hi = d * float(sc_hi) * 0.0625f; m_hi = -(dmin * float(mn_hi));
     }
     __device__ __forceinline__ uint32_t q(int i) const { return i < 4 ? qa[i] : qb[i - 4]; }
     __device__ __forceinline__ half8 step(int s) const {
         if (s < 4) return decode8(q(2 * s) & 0x0F0F0F0Fu, q(2 * s + 1) & 0x0F0F0F0Fu, d_lo, m_lo);
-        return decode8((q(2 * s - 8) >> 4) & 0x0F0F0F0Fu, (q(2 * s - 7) >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
+        return decode8(q(2 * s - 8) & 0xF0F0F0F0u, q(2 * s - 7) & 0xF0F0F0F0u, d_hi, m_hi);
     }
 };
 

@@ -97,13 +97,13 @@ struct ProdQ4K {
         const uint32_t sc_hi = (h1 & mh) | ((a1 >> sa) & ma), mn_hi = ((h1 >> 4) & mh) | ((m1 >> sa) & ma);
         d_lo = d * float(sc_lo);
         m_lo = -(dmin * float(mn_lo));
-        d_hi = d * float(sc_hi);
+        d_hi = d * float(sc_hi) * 0.0625f;  // high nibbles converted in place (16 q), as FragQ4K
         m_hi = -(dmin * float(mn_hi));
     }
     __device__ __forceinline__ half8 chunk(int s) const {
         const int w = 2 * (s & 1);
         if (s < 2) return decode8(qs[w] & 0x0F0F0F0Fu, qs[w + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
-        return decode8((qs[w] >> 4) & 0x0F0F0F0Fu, (qs[w + 1] >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
+        return decode8(qs[w] & 0xF0F0F0F0u, qs[w + 1] & 0xF0F0F0F0u, d_hi, m_hi);
     }
 };
 
