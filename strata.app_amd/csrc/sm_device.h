@@ -133,6 +133,34 @@ __device__ __forceinline__ half8 decode8(uint32_t w0, uint32_t w1, float scale, 
 // mapping, so the product covers every K value exactly once.
 // ---------------------------------------------------------------------------------------
 
+// Scale and bias of Q4_K pairs 2g (low nibbles) and 2g + 1 (high nibbles) from a block's first
+// 16 bytes: f16 d, f16 dmin, scales[12] = bytes b0..b11 (hdr[1..3]). Pair j < 4: scale =
+// b[j] & 63, min = b[j+4] & 63; pair j >= 4: scale = (b[j+4] & 15) | (b[j-4] >> 6) << 4, min =
+// (b[j+4] >> 4) | (b[j] >> 6) << 4 (dequant.hpp:157-190). The four 6-bit fields land in the
+// bytes of one dword {scale 2g, scale 2g+1, min 2g, min 2g+1}: a byte permute gathers
+// X = {b[2g], b[2g+1], b[2g+4], b[2g+5]} (g < 2) or {b[2g+4], b[2g+5]} twice (g >= 2) and
+// Y = {b[2g-4], b[2g-3], b[2g], b[2g+1]}; then V = (X & m1) | ((X >> 4) & m3) | ((Y >> 2) & m2)
+// with (m1, m3, m2) = (0x3F3F3F3F, 0, 0) for g < 2 and (0x0F0F, 0x0F0F0000, 0x30303030) for
+// g >= 2, since (y >> 2) & 0x30 == (y >> 6) << 4 for a byte y. The high-nibble scale is
+// divided by 16 (exact in F32: d * scale >= 2^-24): those values are converted in place as
+// 16 * q (q & 0xF0), so fma(d_hi / 16, 16 q, m_hi) is the same single rounding of
+// d_hi * q + m_hi.
+__device__ __forceinline__ void q4k_pair_scales(const u32x4& hdr, uint32_t g, float& d_lo, float& m_lo, float& d_hi,
+                                                float& m_hi) {
+    const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
+    const bool hi_pairs = g >= 2u;
+    const uint32_t sel_lo = (g & 1u) ? 0x07060302u : 0x05040100u;   // bytes of {hdr[2], hdr[1]}
+    const uint32_t sel_x = hi_pairs ? ((g & 1u) ? 0x03020302u : 0x01000100u) : sel_lo;
+    const uint32_t x = __builtin_amdgcn_perm(hi_pairs ? hdr[3] : hdr[2], hi_pairs ? hdr[3] : hdr[1], sel_x);
+    const uint32_t y = __builtin_amdgcn_perm(hdr[2], hdr[1], sel_lo);
+    const uint32_t v = (x & (hi_pairs ? 0x00000F0Fu : 0x3F3F3F3Fu)) | ((x >> 4) & (hi_pairs ? 0x0F0F0000u : 0u)) |
+                       ((y >> 2) & (hi_pairs ? 0x30303030u : 0u));
+    d_lo = d * ubyte(v, 0);
+    d_hi = d * ubyte(v, 1) * 0.0625f;
+    m_lo = -(dmin * ubyte(v, 2));
+    m_hi = -(dmin * ubyte(v, 3));
+}
+
 // Q4_K (144 B / 256): f16 d, f16 dmin, scales[12] (6-bit scale/min pairs), q[128] nibbles.
 // Values 64g..64g+31 are the low nibbles of q[32g..32g+31] with pair 2g; values
 // 64g+32..64g+63 the high nibbles with pair 2g+1 (dequant.hpp:157-190).
@@ -147,34 +175,7 @@ struct FragQ4K {
         qa = M::template ld<u32x4>(sb + 16 + 32 * grp);
         qb = M::template ld<u32x4>(sb + 32 + 32 * grp);
     }
-    __device__ __forceinline__ void prepare() {
-        const float d = f16_lo(hdr[0]);
-        const float dmin = f16_hi(hdr[0]);
-        // scales[12] = bytes 4..15 of the block = hdr[1..3]. Pair j < 4: scale = b[j] & 63,
-        // min = b[j+4] & 63; pair j >= 4: scale = (b[j+4] & 15) | (b[j-4] >> 6) << 4,
-        // min = (b[j+4] >> 4) | (b[j] >> 6) << 4. Lane group g uses pairs 2g, 2g+1. Both forms
-        // are one mask-and-shift recipe with per-lane constants (no divergent branch):
-        //   scale = (h & mh) | ((a >> sa) & ma),  min = ((h >> 4) & mh) | ((m >> sa) & ma)
-        // with a = b[j] / b[j-4], m = b[j+4] / b[j], h = b[j+4] (pairs 4-7 only), and
-        // (mh, sa, ma) = (0, 0, 63) for pairs 0-3, (15, 2, 48) for pairs 4-7, since
-        // (x >> 2) & 48 == (x >> 6) << 4 for a byte x.
-        const uint32_t lo4 = hdr[1], mid4 = hdr[2], hi4 = hdr[3];  // bytes 0-3, 4-7, 8-11
-        const uint32_t sh0 = 16u * (uint32_t(g) & 1u);              // byte (2g mod 4); +8 for the pair's second
-        const uint32_t up = uint32_t(g) >> 1;                       // 0: pairs 0-3, 1: pairs 4-7
-        const uint32_t mh = 15u * up, sa = 2u * up, ma = 63u - 15u * up;
-        const uint32_t a0 = lo4 >> sh0, a1 = lo4 >> (sh0 + 8u);      // b[j] or b[j-4] in the low byte
-        const uint32_t m0 = mid4 >> sh0, m1 = mid4 >> (sh0 + 8u);    // b[j+4] or b[j]
-        const uint32_t h0 = hi4 >> sh0, h1 = hi4 >> (sh0 + 8u);      // b[j+4] for pairs 4-7
-        const uint32_t sc_lo = (h0 & mh) | ((a0 >> sa) & ma);
-        const uint32_t mn_lo = ((h0 >> 4) & mh) | ((m0 >> sa) & ma);
-        const uint32_t sc_hi = (h1 & mh) | ((a1 >> sa) & ma);
-        const uint32_t mn_hi = ((h1 >> 4) & mh) | ((m1 >> sa) & ma);
-        d_lo = d * float(sc_lo); m_lo = -(dmin * float(mn_lo));
-        // The high nibbles are converted in place (q & 0xF0, i.e. 16 * nibble) and scaled by
-        // d_hi / 16, exact in F32 (d_hi >= 2^-24), so fma(d_hi / 16, 16 q, m_hi) is the same
-        // single rounding of d_hi * q + m_hi and the shift per dword is saved.
-        d_hi = d * float(sc_hi) * 0.0625f; m_hi = -(dmin * float(mn_hi));
-    }
+    __device__ __forceinline__ void prepare() { q4k_pair_scales(hdr, uint32_t(g), d_lo, m_lo, d_hi, m_hi); }
     __device__ __forceinline__ uint32_t q(int i) const { return i < 4 ? qa[i] : qb[i - 4]; }
     __device__ __forceinline__ half8 step(int s) const {
         if (s < 4) return decode8(q(2 * s) & 0x0F0F0F0Fu, q(2 * s + 1) & 0x0F0F0F0Fu, d_lo, m_lo);

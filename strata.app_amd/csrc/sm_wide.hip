@@ -85,21 +85,7 @@ struct ProdQ4K {
         hdr = ld_global<u32x4>(sb);
         qs = ld_global<u32x4>(sb + 16 + 32 * grp + 16 * b);
     }
-    __device__ __forceinline__ void prepare() {
-        const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
-        // Pairs 2g and 2g + 1 by the mask-and-shift recipe of FragQ4K::prepare.
-        const uint32_t sh0 = 16u * (g & 1u), up = g >> 1;
-        const uint32_t mh = 15u * up, sa = 2u * up, ma = 63u - 15u * up;
-        const uint32_t a0 = hdr[1] >> sh0, a1 = hdr[1] >> (sh0 + 8u);
-        const uint32_t m0 = hdr[2] >> sh0, m1 = hdr[2] >> (sh0 + 8u);
-        const uint32_t h0 = hdr[3] >> sh0, h1 = hdr[3] >> (sh0 + 8u);
-        const uint32_t sc_lo = (h0 & mh) | ((a0 >> sa) & ma), mn_lo = ((h0 >> 4) & mh) | ((m0 >> sa) & ma);
-        const uint32_t sc_hi = (h1 & mh) | ((a1 >> sa) & ma), mn_hi = ((h1 >> 4) & mh) | ((m1 >> sa) & ma);
-        d_lo = d * float(sc_lo);
-        m_lo = -(dmin * float(mn_lo));
-        d_hi = d * float(sc_hi) * 0.0625f;  // high nibbles converted in place (16 q), as FragQ4K
-        m_hi = -(dmin * float(mn_hi));
-    }
+    __device__ __forceinline__ void prepare() { q4k_pair_scales(hdr, g, d_lo, m_lo, d_hi, m_hi); }
     __device__ __forceinline__ half8 chunk(int s) const {
         const int w = 2 * (s & 1);
         if (s < 2) return decode8(qs[w] & 0x0F0F0F0Fu, qs[w + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
