@@ -269,10 +269,14 @@ __device__ __forceinline__ uint32_t scan_wide_units(const RoutedGemm& g, uint32_
 // The workgroup's share of the U units' items (unit x column tile). DENSE: the rows are the
 // n_entries activation rows themselves (the shared expert), in units of 256 consecutive rows;
 // the weights are dw0/dw1 and the down output row is the unit row.
-template <class Prod, int MODE, bool DENSE>
+// DYN (a phase that starts at different times on different workgroups): the items of XCD x's
+// range are drawn from counter x of g.counters (zeroed by the stage's plan check) instead of
+// the static order; thread 0 draws the next item when it starts the current one and publishes
+// it in *s_next at the end, so the atomic's round trip overlaps the item.
+template <class Prod, int MODE, bool DENSE, bool DYN = false>
 __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* dw0, const uint8_t* dw1, uint32_t n_ct, uint32_t U,
                            const uint32_t* s_pref, uint8_t (&s_a)[2][kStageBytes], uint8_t (&s_b)[2][kStageBytes],
-                           int32_t* s_dst) {
+                           int32_t* s_dst, uint32_t* s_next = nullptr) {
     constexpr int SB = Prod::kSlab;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const Plan* p = g.plan;
@@ -301,7 +305,14 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
     const uint32_t vx = u_end - u_begin;
     const uint32_t n_items = vx * n_ct;
     const uint32_t nK = g.k / kStepK;
-    for (uint32_t m = l; m < n_items; m += P) {
+    uint32_t* counter = g.counters + x;
+    if (DYN && tid == 0) *s_next = atomicAdd(counter, 1u);
+    for (uint32_t m_static = l;; m_static += P) {
+        __syncthreads();  // the previous item's last reads of LDS are done; *s_next is visible
+        const uint32_t m = DYN ? *s_next : m_static;
+        if (m >= n_items) break;
+        uint32_t next = 0;
+        if (DYN && tid == 0) next = atomicAdd(counter, 1u);
         const uint32_t v = m / n_ct, ct = m - v * n_ct, uidx = u_begin + v;
         Unit u;
         if (DENSE) {
@@ -321,7 +332,6 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
             u.ex = uint32_t(p->grp_e[lo_g]);
         }
         const uint32_t nrows = u.a1 - u.a0;
-        __syncthreads();  // the previous item's last reads of LDS are done
         if (!DENSE && MODE == kDown && tid < kUnitRows) s_dst[tid] = tid < nrows ? g.dst[u.a0 + tid] : -1;
         const uint8_t* w0 = dw0;
         const uint8_t* w1 = dw1;
@@ -335,6 +345,7 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
             __syncthreads();
             if (tid == 0) atomicOr(g.status, fault);
             zero_item<MODE>(g, u, ct, s_dst);
+            if (DYN && tid == 0) *s_next = next;
             continue;
         }
 
@@ -487,6 +498,7 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
         if (nrows == kUnitRows) store_rows(std::true_type());  // workgroup-uniform
         else store_rows(std::false_type());
         if (!DENSE && MODE == kDown && any_bad) atomicOr(g.status, 2u);
+        if (DYN && tid == 0) *s_next = next;  // every thread read *s_next before the item's first barrier
     }
 }
 
@@ -512,7 +524,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(RoutedGemm g, c
 // wide units' items (as the wide kernel), then draws 64-row tile items of the smaller groups
 // from the per-XCD counters, so workgroups with one wide item fewer take more tiles and the
 // tiles fill the wide units' last round (without wide units the tiles are taken in the static
-// order). Down: the tiles first, in the static order, then the wide units. A down tile item
+// order). Down: the tiles first, in the static order, then the wide units, drawn from the
+// per-XCD counters (workgroups leave the tile phase at different times). A down tile item
 // streams its expert's whole weight matrix through L2, which would evict the activation rows
 // that concurrently running wide units share across column tiles; taken first, the tiles
 // overlap the wide units only at the boundary.
@@ -524,7 +537,7 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
         WideSmem w;
         TileSmem<Frag, 2> t;
     } sm;
-    __shared__ uint32_t s_pref_w[513], s_pref_t[513], s_wsum[8], s_flag;
+    __shared__ uint32_t s_pref_w[513], s_pref_t[513], s_wsum[8], s_flag, s_next_w;
     const uint32_t flag = scan_wide_units(g, s_pref_w, s_wsum, &s_flag);
     scan_small_tiles(g, s_pref_t, s_wsum, &s_flag);
     if (flag & 2u) {
@@ -540,7 +553,9 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
     } else {
         tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
         __syncthreads();  // the tile phase's LDS is free
-        wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
+        // Workgroups leave the tile phase at different times: the wide items are drawn.
+        wide_items<Prod, MODE, false, true>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst,
+                                            &s_next_w);
     }
 }
 
