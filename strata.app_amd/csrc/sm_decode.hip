@@ -588,6 +588,24 @@ __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
     constexpr uint32_t NW = GATE_UP ? 2u : 1u;
     constexpr uint32_t VPC = WT == kWF32 ? 4u : 8u;  // values per 16-byte chunk
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    // The T activation rows ([rows][k], F16 or F32) are staged in LDS once per workgroup: every
+    // weight chunk meets all T rows, and LDS reads cost far less issue than a global load per
+    // (chunk, row). The copy is LDS-DMA, 1 KB per wave instruction (the allocation is rounded up
+    // to whole kilobytes; lanes past the rows' end re-read their last 16 bytes into that tail),
+    // issued before the first weight loads so that both are one round trip.
+    extern __shared__ __attribute__((aligned(1024))) uint8_t x_lds[];
+    {
+        const uint32_t xbytes = m.rows * m.k * (XF32 ? 4u : 2u);  // k % 64 == 0: whole 16-byte pieces
+        const uint8_t* xg = reinterpret_cast<const uint8_t*>(m.x);
+        for (uint32_t q = wave; q < (xbytes + 1023u) / 1024u; q += 4u) {
+            const uint32_t off = 1024u * q + 16u * lane;
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const __attribute__((address_space(1))) void*>(
+                    reinterpret_cast<uintptr_t>(xg + (off < xbytes ? off : xbytes - 16u))),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(x_lds + 1024u * q)),
+                16, 0, 0);
+        }
+    }
     const uint32_t nch = m.k / VPC;
     const uint32_t per_lane = (nch + LPR - 1u) / LPR;
     const uint32_t row = matvec_rows_per_block(LPR) * blockIdx.x + wave * RPW + lane / LPR;
@@ -598,20 +616,30 @@ __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
     for (uint32_t w = 0; w < NW; ++w)
 #pragma unroll
         for (uint32_t t = 0; t < 8u; ++t) acc[w][t] = 0.0f;
+    const uint8_t* wr[2] = {m.w0 + uint64_t(row_ok ? row : 0u) * m.k * wbytes,
+                            GATE_UP ? m.w1 + uint64_t(row_ok ? row : 0u) * m.k * wbytes : nullptr};
+    // Chunks in flight per lane (at most): ten for the router's F32 rows, eight for F16/BF16
+    // rows, so the rows of the reference model's widths (2560 values: ten F32 or five F16 chunks
+    // per lane of a 64-lane row) are one round trip.
+    constexpr uint32_t NB = WT == kWF32 ? 10u : 8u;
+    u32x4 raw[NW][NB];
+    auto load_batch = [&](uint32_t base) {
+#pragma unroll
+        for (uint32_t i = 0; i < NB; ++i) {
+            const uint32_t c = lane % LPR + LPR * (base + i);
+            if (c < nch)
+#pragma unroll
+                for (uint32_t w = 0; w < NW; ++w) raw[w][i] = ld_global<u32x4>(wr[w] + 16u * c);
+        }
+    };
+    if (row_ok) load_batch(0u);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows (and the first weights)
+    __syncthreads();
     if (row_ok) {
-        const uint8_t* wr[2] = {m.w0 + uint64_t(row) * m.k * wbytes,
-                                GATE_UP ? m.w1 + uint64_t(row) * m.k * wbytes : nullptr};
-        for (uint32_t base = 0; base < per_lane; base += kPerLane) {
-            u32x4 raw[NW][kPerLane];
+        for (uint32_t base = 0; base < per_lane; base += NB) {
+            if (base > 0u) load_batch(base);
 #pragma unroll
-            for (uint32_t i = 0; i < kPerLane; ++i) {
-                const uint32_t c = lane % LPR + LPR * (base + i);
-                if (c < nch)
-#pragma unroll
-                    for (uint32_t w = 0; w < NW; ++w) raw[w][i] = ld_global<u32x4>(wr[w] + 16u * c);
-            }
-#pragma unroll
-            for (uint32_t i = 0; i < kPerLane; ++i) {
+            for (uint32_t i = 0; i < NB; ++i) {
                 const uint32_t c = lane % LPR + LPR * (base + i);
                 if (c >= nch) continue;
                 float wv[NW][VPC];
@@ -635,30 +663,31 @@ __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
                     if (t >= m.rows) break;
                     float xv[VPC];
                     if (XF32) {
-                        const float* xp = reinterpret_cast<const float*>(m.x) + uint64_t(t) * m.k + VPC * c;
-                        const float4v a = ld_global<float4v>(xp);
+                        const float* xp = reinterpret_cast<const float*>(x_lds) + t * m.k + VPC * c;
+                        const float4v a = *reinterpret_cast<const float4v*>(xp);
 #pragma unroll
                         for (uint32_t j = 0; j < 4u; ++j) xv[j] = a[j];
                         if (VPC == 8u) {
-                            const float4v b = ld_global<float4v>(xp + 4);
+                            const float4v b = *reinterpret_cast<const float4v*>(xp + 4);
 #pragma unroll
                             for (uint32_t j = 0; j < 4u; ++j) xv[(4u + j) % VPC] = b[j];
                         }
                     } else {
-                        const uint8_t* xp = reinterpret_cast<const uint8_t*>(m.x) + (uint64_t(t) * m.k + VPC * c) * 2u;
+                        const uint8_t* xp = x_lds + (t * m.k + VPC * c) * 2u;
                         if (VPC == 8u) {
-                            const u32x4 q = ld_global<u32x4>(xp);
+                            const u32x4 q = *reinterpret_cast<const u32x4*>(xp);
 #pragma unroll
                             for (uint32_t j = 0; j < 4u; ++j) {
                                 xv[(2u * j) % VPC] = f16_lo(q[j]);
                                 xv[(2u * j + 1u) % VPC] = f16_hi(q[j]);
                             }
                         } else {
-                            const uint32_t q0 = ld_global<uint32_t>(xp), q1 = ld_global<uint32_t>(xp + 4);
-                            xv[0] = f16_lo(q0);
-                            xv[1] = f16_hi(q0);
-                            xv[2 % VPC] = f16_lo(q1);
-                            xv[3 % VPC] = f16_hi(q1);
+                            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                            const u32x2 q = *reinterpret_cast<const u32x2*>(xp);
+                            xv[0] = f16_lo(q[0]);
+                            xv[1] = f16_hi(q[0]);
+                            xv[2 % VPC] = f16_lo(q[1]);
+                            xv[3 % VPC] = f16_hi(q[1]);
                         }
                     }
 #pragma unroll
@@ -695,13 +724,27 @@ hipError_t launch_dense_decode_t(const DenseDecode& m, hipStream_t s) {
     // Extra workgroups: the gate logit (shared gate/up) or the snapshot copies (router).
     const uint32_t extra = GATE_UP ? (m.gv != nullptr ? 1u : 0u) : (m.snap_words + m.snap_words2 + 255u) / 256u;
     const dim3 grid(mm.row_blocks + extra);
+    // The staged activation rows: rows x k values, at most 8 x SM_DECODE_MAX_WIDTH F32 (128 KB),
+    // rounded up to whole kilobytes (the copy's unit).
+    const size_t lds = (size_t(m.rows) * m.k * (XF32 ? 4u : 2u) + 1023u) & ~size_t(1023);
+    if (lds > 131072u) return hipErrorInvalidValue;
+    auto go = [&](auto kern) {
+        // Above 64 KB of dynamic LDS the launch needs the kernel's limit raised first (the
+        // widest rows only: T = 8 at K >= 2048 with F32 rows, or K = 4096 with F16 rows).
+        if (lds > 65536u) {
+            const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+            if (attr != hipSuccess) return attr;
+        }
+        kern<<<grid, 256, lds, s>>>(mm);
+        return hipGetLastError();
+    };
     switch (lpr) {
-        case 64: dense_decode_kernel<WT, GATE_UP, XF32, 64><<<grid, 256, 0, s>>>(mm); break;
-        case 32: dense_decode_kernel<WT, GATE_UP, XF32, 32><<<grid, 256, 0, s>>>(mm); break;
-        case 16: dense_decode_kernel<WT, GATE_UP, XF32, 16><<<grid, 256, 0, s>>>(mm); break;
-        default: dense_decode_kernel<WT, GATE_UP, XF32, 8><<<grid, 256, 0, s>>>(mm); break;
+        case 64: return go(dense_decode_kernel<WT, GATE_UP, XF32, 64>);
+        case 32: return go(dense_decode_kernel<WT, GATE_UP, XF32, 32>);
+        case 16: return go(dense_decode_kernel<WT, GATE_UP, XF32, 16>);
+        default: return go(dense_decode_kernel<WT, GATE_UP, XF32, 8>);
     }
-    return hipGetLastError();
 }
 
 // ---- post ops ----------------------------------------------------------------------------

@@ -256,7 +256,9 @@ def test_swiglu_combine_bit_exact(moe, orc, gpu_ctx, stream):
         assert np.array_equal(gu.host(bo, np.float32).reshape(T, d).view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt,T,d,Is", [(4, 8, 2560, 640), (5, 3, 4096, 1536), (4, 1, 2048, 512)])
+# (4, 8, 4096, 4096): the widest rows, whose staged activations need more than 64 KB of LDS
+# (the shared down's F32 hidden rows, 8 x 4096 x 4 bytes).
+@pytest.mark.parametrize("fmt,T,d,Is", [(4, 8, 2560, 640), (5, 3, 4096, 1536), (4, 1, 2048, 512), (4, 8, 4096, 4096)])
 def test_shared_ffn_against_fp64(moe, orc, gpu_ctx, stream, fmt, T, d, Is):
     print(f"case decode shared fmt={fmt} T={T} d={d} Is={Is}", flush=True)
     gen = moe.synth_normal_bf16 if fmt == moe.BF16 else moe.synth_normal_f16
