@@ -380,9 +380,10 @@ struct UnitQ2K {  // 84 B: scales[16] @0, q[64] @16, d @80, dmin @82; 4-byte ali
 };
 
 // ---- grouped mat-vecs --------------------------------------------------------------------
-// Group g = blockIdx.y (blocks past n_groups exit). LPR lanes share a weight row (the
-// smallest power of two covering its units), each lane taking one whole unit, so a row's
-// bytes are all in flight at once and every byte loaded is used. A workgroup takes `iters`
+// Group g = blockIdx.y (blocks past n_groups exit). LPR lanes share a weight row (its unit
+// count where that is 6 or 10, which leaves 4 of a wave's 64 lanes idle, else the smallest
+// power of two covering its units), each lane taking one whole unit, so a row's bytes are all
+// in flight at once and every byte loaded is used. A workgroup takes `iters`
 // consecutive slices of 4 * 64/LPR rows of the stage (gate/up: gate rows 0..I-1 then up rows
 // I..2I-1; down: output rows 0..d-1), one row per LPR-lane segment of a wave. The group's
 // activation blocks are staged in LDS once. Each lane keeps one accumulator per entry of the
@@ -398,6 +399,7 @@ __host__ __device__ constexpr uint32_t matvec_rows_per_block(uint32_t lpr) { ret
 template <class Unit, int MODE, uint32_t LPR>
 __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  // >= 4 waves per SIMD
     constexpr uint32_t RPW = 64u / LPR, RPI = 4u * RPW;  // rows per wave, rows per slice
+    constexpr bool kPow2 = (LPR & (LPR - 1u)) == 0u;
     // LDS: codes [entry][block] (8 words), then d [entry][block], then results [slice row][entry]
     extern __shared__ uint32_t act_s[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -465,11 +467,12 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
         return;
     }
     const uint32_t nblk = m.k / 32u, nunit = m.k / Unit::kVals;
-    const uint32_t seg = lane % LPR;
-    const bool unit_ok = seg < nunit;
+    const uint32_t seg = lane % LPR, rin = lane / LPR;
+    const bool lane_ok = rin < RPW;  // lanes past the wave's last whole row segment (LPR 6 or 10) idle
+    const bool unit_ok = lane_ok && seg < nunit;
     const uint32_t u = unit_ok ? seg : nunit - 1u;
     auto row_ptr = [&](uint32_t it) {  // this lane's row of slice it (clamped into the stage)
-        const uint32_t row = r_first + it * RPI + wave * RPW + lane / LPR;
+        const uint32_t row = r_first + it * RPI + wave * RPW + (lane_ok ? rin : 0u);
         const uint32_t rowc = row < n_rows ? row : n_rows - 1u;
         const bool up = MODE == kGateUp && rowc >= m.out_width;
         return (up ? w1 : w0) + uint64_t(up ? rowc - m.out_width : rowc) * m.row_bytes;
@@ -486,7 +489,7 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
     }
     __syncthreads();
     for (uint32_t it = 0; it < m.iters; ++it) {
-        const uint32_t lr = it * RPI + wave * RPW + lane / LPR;
+        const uint32_t lr = it * RPI + wave * RPW + (lane_ok ? rin : 0u);
         uint32_t r[Unit::kRaw];
         Unit::raw(row_ptr(it), u, r);
         // One entry at a time (n_e is uniform over the workgroup): the unit's sub-blocks against
@@ -515,9 +518,19 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
                     if (sb & 1u) __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            if constexpr (kPow2) {
 #pragma unroll
-            for (uint32_t o = LPR / 2u; o > 0u; o >>= 1) acc = acc + __shfl_xor(acc, int(o));
-            if (seg == 0u) res_s[lr * m.max_group + c] = acc;
+                for (uint32_t o = LPR / 2u; o > 0u; o >>= 1) acc = acc + __shfl_xor(acc, int(o));
+            } else {
+                // A tree within the row's segment: at stride o, segment lane s (s % 2o == 0) adds
+                // lane s + o when that lies inside the segment; the sum ends in segment lane 0.
+#pragma unroll
+                for (uint32_t o = 1u; o < LPR; o <<= 1) {
+                    const float v = __shfl(acc, int(lane + o < 64u ? lane + o : 63u));
+                    if (seg % (2u * o) == 0u && seg + o < LPR) acc = acc + v;
+                }
+            }
+            if (lane_ok && seg == 0u) res_s[lr * m.max_group + c] = acc;
         }
     }
     __syncthreads();  // every slice's rows are in LDS
@@ -790,6 +803,7 @@ hipError_t launch_matvec_t(const DecodeMatvec& mm, hipStream_t s) {
     uint32_t lpr = 1;
     while (lpr < nunit) lpr <<= 1;
     if (lpr < 8u) lpr = 8u;
+    if (nunit == 10u || nunit == 6u) lpr = nunit;  // 60 of 64 lanes busy instead of 40 or 48
     // Slices per workgroup: up to 4 once the groups (at most one per routed entry) give the
     // chip about four workgroups per CU without them; one when there are few groups (T = 1).
     const uint32_t rpi = matvec_rows_per_block(lpr);
@@ -802,6 +816,8 @@ hipError_t launch_matvec_t(const DecodeMatvec& mm, hipStream_t s) {
         case 64: moe_matvec_kernel<Unit, MODE, 64><<<grid, 256, lds, s>>>(m); break;
         case 32: moe_matvec_kernel<Unit, MODE, 32><<<grid, 256, lds, s>>>(m); break;
         case 16: moe_matvec_kernel<Unit, MODE, 16><<<grid, 256, lds, s>>>(m); break;
+        case 10: moe_matvec_kernel<Unit, MODE, 10><<<grid, 256, lds, s>>>(m); break;
+        case 6: moe_matvec_kernel<Unit, MODE, 6><<<grid, 256, lds, s>>>(m); break;
         default: moe_matvec_kernel<Unit, MODE, 8><<<grid, 256, lds, s>>>(m); break;
     }
     return hipGetLastError();
