@@ -545,17 +545,24 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
         return;
     }
     const uint32_t U = s_pref_w[512];
+    // Without wide units (U == 0, workgroup-uniform) the wide phase is skipped whole: its setup
+    // (per-thread constants, some of them spilled at entry) would run for nothing.
     if (MODE == kGateUp) {
-        wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
-        __syncthreads();  // the wide phase's LDS is free
-        if (U > 0u) tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
-        else tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+        if (U > 0u) {
+            wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
+            __syncthreads();  // the wide phase's LDS is free
+            tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+        } else {
+            tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+        }
     } else {
         tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
-        __syncthreads();  // the tile phase's LDS is free
-        // Workgroups leave the tile phase at different times: the wide items are drawn.
-        wide_items<Prod, MODE, false, true>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst,
-                                            &s_next_w);
+        if (U > 0u) {
+            __syncthreads();  // the tile phase's LDS is free
+            // Workgroups leave the tile phase at different times: the wide items are drawn.
+            wide_items<Prod, MODE, false, true>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b,
+                                                sm.w.s_dst, &s_next_w);
+        }
     }
 }
 
