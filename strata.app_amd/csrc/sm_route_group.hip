@@ -12,21 +12,24 @@ constexpr float kWeightFloor = 6.103515625e-5f;  // 2^-14
 // ---------------------------------------------------------------------------------------
 // Router GEMM: logits[t,e] = sum_k x[t,k] * W[e,k], F16 activations, F32 weights.
 // Each F32 weight is split into an F16 head and an F16 tail scaled by 2^11
-// (w = hi + lo * 2^-11 to ~2^-24 relative); two MFMA accumulators carry the head and tail
-// products and are merged as fma(lo, 2^-11, hi). Tile: ROWS tokens (32, 64 or 128) x 64
-// experts per 256-thread workgroup; wave w owns experts 16w..16w+15. Each expert's weights
-// are read and split once per workgroup, so larger token tiles divide that work; the
-// launcher takes the largest tile that still gives every CU a workgroup.
+// (w = hi + lo * 2^-11 to about 2^-22 relative); two MFMA accumulators carry the head and
+// tail products and are merged as fma(lo, 2^-11, hi). Tile: ROWS tokens (32, 64 or 128) x
+// 64 experts per 512-thread workgroup. Wave w owns experts 16 (w & 3) .. +15 and, of each
+// 64-column stage, the 32-column k-step w >> 2, so the two waves of a SIMD multiply the same
+// experts over different columns and their partial sums are added once at the end (through
+// LDS). Each expert's weights are read and split once per workgroup, so larger token tiles
+// divide that work; the launcher takes the largest tile that still gives every CU a
+// workgroup.
 // The reduction is streamed in stages of 64 columns through an LDS ring of NST slots: each
 // stage holds the ROWS x 64 activation slab and the 64 x 64 F32 weight slab, both copied by
-// LDS-DMA (16 bytes per lane, XOR-swizzled chunk positions), and the copies run NST - 1
-// stages ahead, so a wave waits only for the oldest stage while the later ones stay in
-// flight (one workgroup per CU has no other work to hide the memory latency behind). The
-// ring stays within 96 KB so that a workgroup of the shared expert's GEMM, which runs beside
-// the router on the second stream, still fits on the same CU. K-steps keep the order of a
-// plain loop over k, so the sums are those of a one-stage pipeline.
+// LDS-DMA (16 bytes per lane, XOR-swizzled chunk positions) by waves 0-3, and the copies run
+// NST - 1 stages ahead, so a wave waits only for the oldest stage while the later ones stay
+// in flight. The ring stays within 96 KB so that a workgroup of the shared expert's GEMM,
+// which runs beside the router on the second stream, still fits on the same CU. Within a
+// wave the k-steps keep the order of a plain loop over its columns.
 // ---------------------------------------------------------------------------------------
 constexpr int kRouterCols = 64;
+constexpr int kRouterThreads = 512;
 
 template <int ROWS>
 struct RouterStage {
@@ -34,14 +37,17 @@ struct RouterStage {
     static constexpr int NST = ROWS == 128 ? 3 : 4;    // ring slots (NST - 1 stages in flight)
     static constexpr int CPR = KS / 8;                 // 16-byte activation chunks per row
     static constexpr int RPI = 64 / CPR;               // activation rows per copy instruction
-    static constexpr int NA = ROWS / (4 * RPI);        // activation copies per wave and stage
+    static constexpr int NA = ROWS / (4 * RPI);        // activation copies per copying wave and stage
     static constexpr int WCPR = KS / 4;                // 16-byte weight chunks per expert row
     static constexpr int WPI = 64 / WCPR;              // expert rows per copy instruction
-    static constexpr int NW = 16 / WPI;                // weight copies per wave (its 16 experts)
+    static constexpr int NW = 16 / WPI;                // weight copies per copying wave (its 16 experts)
     static constexpr int A_BYTES = ROWS * KS * 2;
     static constexpr int BYTES = A_BYTES + kRouterCols * KS * 4;
     static_assert(NA * 4 * RPI == ROWS && NW * WPI == 16, "copy map covers the stage");
     static_assert(NST * BYTES <= 96 * 1024, "LDS ring leaves room for a co-resident workgroup");
+    // The second k-half's partial sums (ROWS / 16 blocks x 4 values x head and tail, for
+    // 256 lanes) pass through the ring after the last stage.
+    static_assert(ROWS / 16 * 8 * 256 * 4 <= NST * BYTES, "partial sums fit the ring");
 };
 
 // s_waitcnt immediate that waits for at most n vector-memory operations (gfx9 encoding:
@@ -49,15 +55,19 @@ struct RouterStage {
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 template <int ROWS>
-__global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __restrict__ x,
-                                                          const float* __restrict__ w,
-                                                          const float* __restrict__ bias,
-                                                          float* __restrict__ logits,
-                                                          uint32_t rows, uint32_t d, uint32_t E) {
+__global__ __launch_bounds__(kRouterThreads) void router_gemm_kernel(const _Float16* __restrict__ x,
+                                                                    const float* __restrict__ w,
+                                                                    const float* __restrict__ bias,
+                                                                    float* __restrict__ logits,
+                                                                    uint32_t rows, uint32_t d, uint32_t E) {
     using S = RouterStage<ROWS>;
     constexpr int RB = ROWS / 16;  // 16-row MFMA blocks
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
     __shared__ __attribute__((aligned(1024))) uint8_t ring[S::NST * S::BYTES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = (tid >> 6) & 3, kh = tid >> 8;  // expert quarter, k-half of each stage
+    const bool copier = kh == 0;
     const int n = lane & 15, g = lane >> 4;
     const uint32_t t0 = blockIdx.x * ROWS;
     const uint32_t e0 = blockIdx.y * kRouterCols;
@@ -75,8 +85,8 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
         aofs[j] = uint64_t(t) * d + 8u * C;
     }
     // Weight copy q = NW*wave + j: expert row Rw = WPI*q + lane / WCPR of the tile (wave w
-    // copies its own 16 experts), position p = lane % WCPR holding chunk p ^ (Rw & 15).
-    // Row 0 stands in for experts past E; those outputs are never stored.
+    // copies the 16 experts of its quarter), position p = lane % WCPR holding chunk
+    // p ^ (Rw & 15). Row 0 stands in for experts past E; those outputs are never stored.
     uint64_t wofs[S::NW];
 #pragma unroll
     for (int j = 0; j < S::NW; ++j) {
@@ -106,55 +116,83 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const _Float16* __rest
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) { acc_hi[rb] = float4v{0, 0, 0, 0}; acc_lo[rb] = float4v{0, 0, 0, 0}; }
     const uint32_t n_st = d / S::KS;
+    if (copier) {
 #pragma unroll
-    for (int i = 0; i < S::NST - 1; ++i)
-        if (uint32_t(i) < n_st) issue(i, i);
+        for (int i = 0; i < S::NST - 1; ++i)
+            if (uint32_t(i) < n_st) issue(i, i);
+    }
     const uint32_t wrow = 16u * wave + n;  // this lane's expert row in the weight slab
+    const uint32_t c0 = 8u * kh + 2u * g;   // lane group g holds columns 8g .. 8g + 7 of the k-step
     for (uint32_t st = 0; st < n_st; ++st) {
-        // Stage st's copies (of every wave, hence the barrier); stage st + 1 may stay in flight.
-        // A bare s_barrier: __syncthreads() would add a workgroup release that waits for every
-        // copy in flight. This wave's stage-st copies are complete after the wait, and the
-        // slot refilled below was last read in the previous iteration, whose LDS reads every
-        // wave consumed before reaching this barrier.
-        const uint32_t later = n_st - 1u - st;  // stages issued after st (at most NST - 2)
-        if (S::NST == 4 && later >= 2u) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (S::NA + S::NW)));
-        else if (later >= 1u) __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::NA + S::NW));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // Stage st's copies (of every copying wave, hence the barrier); stage st + 1 may stay
+        // in flight. A bare s_barrier: __syncthreads() would add a workgroup release that
+        // waits for every copy in flight. A copying wave's stage-st copies are complete after
+        // the wait, and the slot refilled below was last read in the previous iteration, whose
+        // LDS reads every wave consumed before reaching this barrier.
+        if (copier) {
+            const uint32_t later = n_st - 1u - st;  // stages issued after st (at most NST - 2)
+            if (S::NST == 4 && later >= 2u) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (S::NA + S::NW)));
+            else if (later >= 1u) __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::NA + S::NW));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
         __builtin_amdgcn_s_barrier();
-        if (st + S::NST - 1 < n_st) issue(st + S::NST - 1, (st + S::NST - 1) % S::NST);
+        if (copier && st + S::NST - 1 < n_st) issue(st + S::NST - 1, (st + S::NST - 1) % S::NST);
         const uint8_t* base = ring + (st % S::NST) * S::BYTES;
         const uint8_t* wb = base + S::A_BYTES + wrow * (S::KS * 4);
+        // Every operand read of the k-step first, then the split, so one wait covers them.
+        const float4v w0 = *reinterpret_cast<const float4v*>(wb + 16u * (c0 ^ uint32_t(n)));
+        const float4v w1 = *reinterpret_cast<const float4v*>(wb + 16u * ((c0 + 1u) ^ uint32_t(n)));
+        half8 a[RB];
 #pragma unroll
-        for (int s = 0; s < S::KS / 32; ++s) {
-            // k-step s: lane group g holds columns 32s + 8g .. 32s + 8g + 7 of the stage.
-            const uint32_t c0 = 8u * s + 2u * g;
-            const float4v w0 = *reinterpret_cast<const float4v*>(wb + 16u * (c0 ^ uint32_t(n)));
-            const float4v w1 = *reinterpret_cast<const float4v*>(wb + 16u * ((c0 + 1u) ^ uint32_t(n)));
-            half8 bh, bl;
+        for (int rb = 0; rb < RB; ++rb) {
+            const uint32_t r = 16u * rb + n;
+            const uint32_t pos = (4u * kh + g) ^ (r % S::CPR);
+            a[rb] = *reinterpret_cast<const half8*>(base + r * (S::KS * 2) + 16u * pos);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        half8 bh, bl;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float wf = i < 4 ? w0[i] : w1[i - 4];
-                const _Float16 h = _Float16(wf);
-                bh[i] = h;
-                bl[i] = _Float16((wf - float(h)) * 2048.0f);
-            }
+        for (int i = 0; i < 8; i += 2) {
+            const f2v wv = i < 4 ? f2v{w0[i], w0[i + 1]} : f2v{w1[i - 4], w1[i - 3]};
+            const h2v hp = __builtin_convertvector(wv, h2v);                                     // head, RNE
+            const h2v lp = __builtin_convertvector((wv - __builtin_convertvector(hp, f2v)) * 2048.0f, h2v);  // tail
+            bh[i] = hp.x;
+            bh[i + 1] = hp.y;
+            bl[i] = lp.x;
+            bl[i + 1] = lp.y;
+        }
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                const uint32_t r = 16u * rb + n;
-                const uint32_t pos = (4u * s + g) ^ (r % S::CPR);
-                const half8 a = *reinterpret_cast<const half8*>(base + r * (S::KS * 2) + 16u * pos);
-                acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, acc_hi[rb], 0, 0, 0);
-                acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, acc_lo[rb], 0, 0, 0);
-            }
+        for (int rb = 0; rb < RB; ++rb) {
+            acc_hi[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bh, acc_hi[rb], 0, 0, 0);
+            acc_lo[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bl, acc_lo[rb], 0, 0, 0);
         }
     }
-    if (!e_ok) return;
+    // The second k-half hands its partial sums to the first through the ring (every wave's
+    // last reads of it are done at the barrier).
+    __syncthreads();
+    float* part = reinterpret_cast<float*>(ring);
+    const uint32_t pl = 64u * wave + lane;
+    if (!copier) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                part[(8 * rb + 2 * i) * 256 + pl] = acc_hi[rb][i];
+                part[(8 * rb + 2 * i + 1) * 256 + pl] = acc_lo[rb][i];
+            }
+    }
+    __syncthreads();
+    if (!copier || !e_ok) return;
     const float b = bias != nullptr ? bias[e] : 0.0f;
     float v[RB][4];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[rb][i] = __builtin_fmaf(acc_lo[rb][i], 4.8828125e-4f, acc_hi[rb][i]) + b;
+        for (int i = 0; i < 4; ++i) {
+            const float hi = acc_hi[rb][i] + part[(8 * rb + 2 * i) * 256 + pl];
+            const float lo = acc_lo[rb][i] + part[(8 * rb + 2 * i + 1) * 256 + pl];
+            v[rb][i] = __builtin_fmaf(lo, 4.8828125e-4f, hi) + b;
+        }
     // A full token tile stores without per-row branches, so the bias load is waited for once
     // (a wait per branch would also wait for each earlier store).
     if (t0 + ROWS <= rows) {
@@ -688,11 +726,11 @@ hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bi
     const uint32_t ecols = (E + kRouterCols - 1) / kRouterCols;
     auto blocks = [&](uint32_t r) { return ((rows + r - 1) / r) * ecols; };
     if (blocks(128) >= 256u) {
-        router_gemm_kernel<128><<<dim3((rows + 127) / 128, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+        router_gemm_kernel<128><<<dim3((rows + 127) / 128, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E);
     } else if (blocks(64) >= 256u) {
-        router_gemm_kernel<64><<<dim3((rows + 63) / 64, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+        router_gemm_kernel<64><<<dim3((rows + 63) / 64, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E);
     } else {
-        router_gemm_kernel<32><<<dim3((rows + 31) / 32, ecols), 256, 0, s>>>(x, w, bias, logits, rows, d, E);
+        router_gemm_kernel<32><<<dim3((rows + 31) / 32, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E);
     }
     return hipGetLastError();
 }
