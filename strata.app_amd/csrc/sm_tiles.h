@@ -106,12 +106,11 @@ __device__ __forceinline__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32
 }
 
 // Item `item` (tile k = item / n_chunks of the enumeration, column chunk item % n_chunks):
-// its rows, column tiles and weights. Returns false when the item is done already: an
-// expert without usable weights has zeroed its rows and set status bit 0 (missing) or 2
-// (unleased tiered slot). Uniform per workgroup.
+// its rows, column tiles and weights, and the weight fault code (0: usable). No side
+// effects. Uniform per workgroup.
 template <int MODE>
-__device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item, uint32_t n_ntiles,
-                            uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t) {
+__device__ __forceinline__ uint32_t staged_item_work(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item,
+                                                     uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks, TileWork& t) {
     const Plan* p = g.plan;
     const uint32_t k = item / n_chunks, chunk = item - k * n_chunks;
     uint32_t lo = 0, hi = 512;
@@ -129,7 +128,15 @@ __device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_
     const uint64_t* addr = g.addresses + 3u * ex;
     t.w0 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[0] : addr[2]);
     t.w1 = reinterpret_cast<const uint8_t*>(MODE == kGateUp ? addr[1] : addr[2]);
-    if (const uint32_t fault = weight_fault(t.w0, t.w1)) {
+    return weight_fault(t.w0, t.w1);
+}
+
+// staged_item_work, and false when the item is done already: an expert without usable
+// weights has zeroed its rows and set status bit 0 (missing) or 2 (unleased tiered slot).
+template <int MODE>
+__device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item, uint32_t n_ntiles,
+                            uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t) {
+    if (const uint32_t fault = staged_item_work<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, t)) {
         if (threadIdx.x == 0) atomicOr(g.status, fault);
         zero_cols<MODE>(g, t.a0, t.a1, t.nt_begin * out_per_nt, t.nt_end * out_per_nt, MODE == kDown);
         return false;
@@ -391,6 +398,15 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
     uint32_t* counter = g.counters + x;
     uint32_t item_static = x * per + (blockIdx.x >> 3);
     if (dynamic && threadIdx.x == 0) sm.s_next = x * per + atomicAdd(counter, 1u);
+    // Static order with streamed slabs and two weight images: the next item's work is looked
+    // up at the start of the current one and its first copies are issued in the current
+    // item's last step, into the buffers that step does not read, so an item starts without
+    // the plan, address and copy round trips. Buffers then alternate across items: step s of
+    // an item uses parity (par0 + s) & 1.
+    constexpr bool XPF = !DYNAMIC && !RESIDENT && WBUF == 2;
+    bool pf_have = false;  // the current item's work and first copies came from the previous one
+    TileWork t_pf{};
+    uint32_t par0 = 0;
     for (;; item_static += P) {
     __syncthreads();  // the previous item's reads of LDS are done; s_next is visible
     const uint32_t item = dynamic ? sm.s_next : item_static;
@@ -398,11 +414,17 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
     uint32_t next = 0;
     if (dynamic && threadIdx.x == 0) next = atomicAdd(counter, 1u);
     TileWork t;
-    if (!staged_item<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, S::kOut, t)) {
+    const bool pf = XPF && pf_have;
+    if (pf) {
+        t = t_pf;
+    } else if (!staged_item<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, S::kOut, t)) {
         __syncthreads();  // every thread has read s_next
         if (dynamic && threadIdx.x == 0) sm.s_next = x * per + next;
         continue;
     }
+    TileWork t_nx{};
+    bool nx_ok = false;  // an item whose weights fault is left to its own turn
+    if (XPF && item + P < i_end) nx_ok = staged_item_work<MODE>(g, s_pref, item + P, n_ntiles, npi, n_chunks, t_nx) == 0u;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, gq = lane >> 4;
     // Read once here rather than in each epilogue, where a dependent global load would also
     // wait for the copies of the next step (visible after the first loop barrier).
@@ -417,12 +439,14 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
     // and weight items j with j % 8 == p.
     // Part p (0..7) of the copies of step (nt, sb) into buffer `buf` (computed once per step by
     // the caller: the division by n_slabs stays out of the k-step loop).
-    auto issue_part = [&](uint32_t nt, uint32_t sb, uint32_t buf, int p) {
-        if (!RESIDENT && p < 4) issue_slab_part(asrc, sb * kSlab, sa[buf], wave, p);
+    auto issue_part_of = [&](const TileWork& tw, const _Float16* const (&as)[4], uint32_t nt, uint32_t sb,
+                             uint32_t buf, int p) {
+        if (!RESIDENT && p < 4) issue_slab_part(as, sb * kSlab, sa[buf], wave, p);
         uint8_t* wb = sw[WBUF == 2 ? buf : 0u];
 #pragma unroll
-        for (uint32_t j = uint32_t(p); j < WC::kPerWave; j += 8u) wc.issue(g, t, nt, sb, wb, wave, j);
+        for (uint32_t j = uint32_t(p); j < WC::kPerWave; j += 8u) wc.issue(g, tw, nt, sb, wb, wave, j);
     };
+    auto issue_part = [&](uint32_t nt, uint32_t sb, uint32_t buf, int p) { issue_part_of(t, asrc, nt, sb, buf, p); };
     if (RESIDENT)
         for (uint32_t sb = 0; sb < n_slabs; ++sb) issue_slab(asrc, sb * kSlab, sa[sb], wave);
     constexpr bool DIRECT = DirectWeights<Frag, MODE, RESIDENT>::value;
@@ -523,8 +547,10 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
         if (dynamic && threadIdx.x == 0) sm.s_next = x * per + next;
         continue;
     }
+    if (!pf) {
 #pragma unroll
-    for (int p = 0; p < 8; ++p) issue_part(t.nt_begin, 0u, 0u, p);
+        for (int p = 0; p < 8; ++p) issue_part(t.nt_begin, 0u, par0, p);
+    }
     // The step loop, specialised on the number of 16-row blocks holding entries.
     auto run = [&](auto rb_const) {
         constexpr int RB = decltype(rb_const)::value;
@@ -538,7 +564,8 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's copies ...
             __syncthreads();                                       // ... from every wave
             const bool more = step + 1 < n_steps;
-            const uint8_t* wb = sw[WBUF == 2 ? (step & 1u) : 0u];
+            const uint32_t par = (par0 + step) & 1u;
+            const uint8_t* wb = sw[WBUF == 2 ? par : 0u];
             Frag c[NF];
 #pragma unroll
             for (int f = 0; f < NF; ++f) c[f].template load<FromLds>(wb + S::image_row(wave, n, f) * SB, gq);
@@ -554,11 +581,16 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
             // before the second barrier).
             if (more) {
 #pragma unroll
-                for (int p = 0; p < 8; ++p) issue_part(nx_nt, nx_sb, (step + 1u) & 1u, p);
+                for (int p = 0; p < 8; ++p) issue_part(nx_nt, nx_sb, par ^ 1u, p);
+            } else if (XPF && nx_ok) {
+                const _Float16* asrc_nx[4];
+                slab_sources(g, t_nx, wave, lane, asrc_nx);
+#pragma unroll
+                for (int p = 0; p < 8; ++p) issue_part_of(t_nx, asrc_nx, t_nx.nt_begin, 0u, par ^ 1u, p);
             }
 #pragma unroll
             for (int f = 0; f < NF; ++f) c[f].prepare();
-            slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : (step & 1u)], n, gq, c, acc, [](int) {});
+            slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : par], n, gq, c, acc, [](int) {});
             if (sb == n_slabs - 1u)  // column tile complete
                 staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
             cur_sb = nx_sb;
@@ -570,6 +602,11 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
         case 2: run(std::integral_constant<int, 2>()); break;
         case 3: run(std::integral_constant<int, 3>()); break;
         default: run(std::integral_constant<int, 4>()); break;
+    }
+    if (XPF) {
+        pf_have = nx_ok;
+        t_pf = t_nx;
+        par0 = (par0 + n_steps) & 1u;
     }
     // Every thread read s_next before the item's first step barrier.
     if (dynamic && threadIdx.x == 0) sm.s_next = x * per + next;
