@@ -280,11 +280,20 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     }
     float selected = 0.0f, sel_sum = 0.0f;
     for (uint32_t rank = 0; rank < K; ++rank) {
-        float best = v[0];
-        int32_t who = int32_t(L);
+        // The lane's own argmax as a pairwise tree (depth log2 NV instead of a chain of NV - 1
+        // dependent compares); the left, lower-index side wins ties, so the result is the
+        // first maximum, as a scan in index order gives.
+        float bv[NV];
+        int32_t bw[NV];
 #pragma unroll
-        for (int i = 1; i < NV; ++i)
-            if (v[i] > best) { best = v[i]; who = int32_t(L + 32u * i); }
+        for (int i = 0; i < NV; ++i) { bv[i] = v[i]; bw[i] = int32_t(L + 32u * i); }
+#pragma unroll
+        for (int w = 1; w < NV; w *= 2)
+#pragma unroll
+            for (int i = 0; i + w < NV; i += 2 * w)
+                if (bv[i + w] > bv[i]) { bv[i] = bv[i + w]; bw[i] = bw[i + w]; }
+        float best = bv[0];
+        int32_t who = bw[0];
         argmax_step<0xB1>(best, who);
         argmax_step<0x4E>(best, who);
         argmax_step<0x124>(best, who);
