@@ -35,11 +35,24 @@ static_assert(kArriveBytes + 4 <= kPlanSlotBytes, "arrival word inside the plan 
 enum class Fmt : int { Q8_0 = 1, Q4_K = 2, Q2_K = 3, F16 = 4, BF16 = 5 };
 
 // ---- route ----
+// Duty of the router in a route/gather composition (null: none): it zeroes the grouping
+// histogram's first `hist_words` words (the per-tile counts) and the plan's arrival word, so
+// that top-k counts the routed entries straight into the histogram (launch_route_topk with
+// hist) and the grouping skips its count kernel (launch_grouping with counted).
+struct RouterPrep {
+    uint32_t* hist = nullptr;
+    uint32_t hist_words = 0;
+    uint32_t* arrive = nullptr;
+};
 // bias (F32 [E]) may be null.
 hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bias, float* logits,
-                              uint32_t rows, uint32_t d, uint32_t n_experts, hipStream_t s);
+                              uint32_t rows, uint32_t d, uint32_t n_experts, hipStream_t s,
+                              const RouterPrep* prep = nullptr);
+// hist (may be null): per-tile counts (tiles of kCountTile route-order entries) that each
+// selected entry is added to.
 hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, uint32_t rows,
-                             uint32_t n_experts, uint32_t top_k, int divide, hipStream_t s);
+                             uint32_t n_experts, uint32_t top_k, int divide, hipStream_t s,
+                             uint32_t* hist = nullptr);
 
 // ---- grouping ----
 // hist has ceil(N/256) + 1 rows of n_experts u32; the extra last row holds each expert's
@@ -55,9 +68,12 @@ struct GroupPrep {
 // resident (may be null: full residency): the selected layer's row of the I32 [layer][E]
 // residency table; a group's grp_res is resident[e] >= 0, n_miss counts the other groups and
 // skip = (n_miss == 0).
+// counted: top-k has already counted the entries into hist (RouterPrep), so the count
+// kernel is skipped.
 hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t top_k, uint32_t n_experts,
                            uint32_t* hist, Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst,
-                           const GroupPrep* prep, const int32_t* resident, hipStream_t s);
+                           const GroupPrep* prep, const int32_t* resident, hipStream_t s,
+                           bool counted = false);
 hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
                          const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
 

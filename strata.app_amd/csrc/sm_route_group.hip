@@ -59,7 +59,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_gemm_kernel(const _Floa
                                                                     const float* __restrict__ w,
                                                                     const float* __restrict__ bias,
                                                                     float* __restrict__ logits,
-                                                                    uint32_t rows, uint32_t d, uint32_t E) {
+                                                                    uint32_t rows, uint32_t d, uint32_t E,
+                                                                    RouterPrep prep) {
     using S = RouterStage<ROWS>;
     constexpr int RB = ROWS / 16;  // 16-row MFMA blocks
     typedef float f2v __attribute__((ext_vector_type(2)));
@@ -73,6 +74,12 @@ __global__ __launch_bounds__(kRouterThreads) void router_gemm_kernel(const _Floa
     const uint32_t e0 = blockIdx.y * kRouterCols;
     const uint32_t e = e0 + 16 * wave + n;
     const bool e_ok = e < E;
+    if (prep.hist != nullptr) {  // the grouping histogram's counts, before top-k adds to them
+        const uint32_t nb = gridDim.x * gridDim.y, b = blockIdx.y * gridDim.x + blockIdx.x;
+        for (uint32_t i = b * kRouterThreads + uint32_t(tid); i < prep.hist_words; i += nb * kRouterThreads)
+            prep.hist[i] = 0u;
+        if (b == 0 && tid == 0) *prep.arrive = 0u;
+    }
     // Copy maps (element offsets at k = 0, in 64 bits: rows x d may exceed 2^32).
     // Activation copy q = NA*wave + j fills LDS chunk positions [64q, 64q + 64): row
     // R = RPI*q + lane / CPR, position p = lane % CPR holding chunk p ^ (R % CPR).
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                                                          int32_t* __restrict__ ids,
                                                          float* __restrict__ weights,
                                                          uint32_t rows, uint32_t E, uint32_t K,
-                                                         int divide) {
+                                                         int divide, uint32_t* __restrict__ hist) {
     const uint32_t L = threadIdx.x & 31u;
     const uint32_t t = (blockIdx.x * 256u + threadIdx.x) >> 5;
     const bool live = t < rows;
@@ -308,7 +315,11 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 #pragma unroll
             for (int i = 0; i < NV; ++i)
                 if (i == slot) v[i] = kNegInf;
-            if (live) ids[uint64_t(t) * K + rank] = who;
+            if (live) {
+                const uint64_t entry = uint64_t(t) * K + rank;
+                ids[entry] = who;
+                if (hist != nullptr && uint32_t(who) < E) atomicAdd(&hist[(entry / kCountTile) * E + uint32_t(who)], 1u);
+            }
             sel_sum = sel_sum + best;
         }
         if (rank == L) selected = best;
@@ -729,41 +740,42 @@ __global__ __launch_bounds__(256) void destination_validate_kernel(const int32_t
 }  // namespace
 
 hipError_t launch_router_gemm(const _Float16* x, const float* w, const float* bias, float* logits,
-                              uint32_t rows, uint32_t d, uint32_t E, hipStream_t s) {
+                              uint32_t rows, uint32_t d, uint32_t E, hipStream_t s, const RouterPrep* prep) {
+    const RouterPrep rp = prep != nullptr ? *prep : RouterPrep{};
     // The largest token tile that still launches at least one workgroup per CU (256), so
     // each expert's weights are split as few times as the layer allows.
     const uint32_t ecols = (E + kRouterCols - 1) / kRouterCols;
     auto blocks = [&](uint32_t r) { return ((rows + r - 1) / r) * ecols; };
     if (blocks(128) >= 256u) {
-        router_gemm_kernel<128><<<dim3((rows + 127) / 128, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E);
+        router_gemm_kernel<128><<<dim3((rows + 127) / 128, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E, rp);
     } else if (blocks(64) >= 256u) {
-        router_gemm_kernel<64><<<dim3((rows + 63) / 64, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E);
+        router_gemm_kernel<64><<<dim3((rows + 63) / 64, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E, rp);
     } else {
-        router_gemm_kernel<32><<<dim3((rows + 31) / 32, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E);
+        router_gemm_kernel<32><<<dim3((rows + 31) / 32, ecols), kRouterThreads, 0, s>>>(x, w, bias, logits, rows, d, E, rp);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_route_topk(const float* logits, int32_t* ids, float* weights, uint32_t rows,
-                             uint32_t E, uint32_t K, int divide, hipStream_t s) {
+                             uint32_t E, uint32_t K, int divide, hipStream_t s, uint32_t* hist) {
     const uint32_t blocks = (rows + 7u) / 8u;
     const uint32_t nv = (E + 31u) / 32u;
-    if (nv <= 1) route_topk_kernel<1><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
-    else if (nv <= 2) route_topk_kernel<2><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
-    else if (nv <= 4) route_topk_kernel<4><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
-    else if (nv <= 8) route_topk_kernel<8><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
-    else route_topk_kernel<16><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide);
+    if (nv <= 1) route_topk_kernel<1><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide, hist);
+    else if (nv <= 2) route_topk_kernel<2><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide, hist);
+    else if (nv <= 4) route_topk_kernel<4><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide, hist);
+    else if (nv <= 8) route_topk_kernel<8><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide, hist);
+    else route_topk_kernel<16><<<blocks, 256, 0, s>>>(logits, ids, weights, rows, E, K, divide, hist);
     return hipGetLastError();
 }
 
 hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32_t E, uint32_t* hist,
                            Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst, const GroupPrep* prep,
                            const int32_t* resident,
-                           hipStream_t s) {
+                           hipStream_t s, bool counted) {
     const uint32_t N = rows * K;
     const uint32_t n_tiles = (N + kCountTile - 1) / kCountTile;
     uint32_t* arrive = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(plan) + kArriveBytes);
-    group_count_kernel<<<n_tiles, 256, 0, s>>>(ids, N, E, hist, arrive);
+    if (!counted) group_count_kernel<<<n_tiles, 256, 0, s>>>(ids, N, E, hist, arrive);
     group_scan_plan_kernel<<<(E + 31) / 32, kScanThreads, 0, s>>>(hist, E, N, n_tiles, plan, tiles, arrive,
                                                                   prep != nullptr ? *prep : GroupPrep{}, resident);
     group_scatter_kernel<<<n_tiles, 256, 0, s>>>(ids, N, K, E, n_tiles, hist, src, dst);

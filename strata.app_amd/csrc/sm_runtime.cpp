@@ -271,11 +271,13 @@ bool check_route(Check& c, const sm_moe_shape& s, const sm_route_buffers& b, Rou
     return ok;
 }
 
-void encode_route_launch(sm_segment* seg, const sm_moe_shape& s, int divide, const RouteRes& r) {
+// hist (0: none): the grouping histogram that top-k counts its entries into (route/gather).
+void encode_route_launch(sm_segment* seg, const sm_moe_shape& s, int divide, const RouteRes& r, uintptr_t hist = 0) {
     const auto rows = s.rows, E = s.n_experts, K = s.top_k;
     add_step(seg, "route top-k", [=](hipStream_t st) {
         return sm::launch_route_topk(reinterpret_cast<const float*>(r.logits), reinterpret_cast<int32_t*>(r.ids),
-                                     reinterpret_cast<float*>(r.weights), rows, E, K, divide, st);
+                                     reinterpret_cast<float*>(r.weights), rows, E, K, divide, st,
+                                     reinterpret_cast<uint32_t*>(hist));
     });
 }
 
@@ -338,8 +340,9 @@ struct LayerChecks {
     int slot1, slot2;
 };
 
+// counted: top-k has counted the entries into the histogram already (route/gather).
 void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupRes& r,
-                            const LayerChecks* lc = nullptr) {
+                            const LayerChecks* lc = nullptr, bool counted = false) {
     const auto rows = s.rows, E = s.n_experts, K = s.top_k, d = s.hidden;
     const bool fused = lc != nullptr;
     const sm::GroupPrep prep = fused ? lc->prep : sm::GroupPrep{};
@@ -348,7 +351,7 @@ void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupR
                                    reinterpret_cast<uint32_t*>(r.hist), reinterpret_cast<sm::Plan*>(r.plan),
                                    reinterpret_cast<uint32_t*>(r.tiles), reinterpret_cast<int32_t*>(r.src),
                                    reinterpret_cast<int32_t*>(r.dst), fused ? &prep : nullptr,
-                                   reinterpret_cast<const int32_t*>(r.resident), st);
+                                   reinterpret_cast<const int32_t*>(r.resident), st, counted);
     });
     if (!fused) {
         add_step(seg, "gather", [=](hipStream_t st) {
@@ -1071,13 +1074,18 @@ bool check_route_gather(Check& c, const sm_moe_shape& s, const sm_route_gather_b
 void encode_route_gather_launch(sm_segment* seg, const sm_moe_shape& s, const RouterRes& rr, const RouteRes& ro,
                                 const GroupRes& gr, const LayerChecks* lc = nullptr) {
     const auto rows = s.rows, d = s.hidden, E = s.n_experts;
+    // The router clears the histogram's counts and the arrival word, top-k counts its entries
+    // into the histogram, and the grouping starts at its scan: one launch fewer.
+    const uint32_t n_tiles = uint32_t((uint64_t(rows) * s.top_k + sm::kCountTile - 1) / sm::kCountTile);
+    const sm::RouterPrep rp{reinterpret_cast<uint32_t*>(gr.hist), n_tiles * E,
+                            reinterpret_cast<uint32_t*>(gr.plan + sm::kArriveBytes)};
     add_step(seg, "router GEMM", [=](hipStream_t st) {
         return sm::launch_router_gemm(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
                                       reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits),
-                                      rows, d, E, st);
+                                      rows, d, E, st, &rp);
     });
-    encode_route_launch(seg, s, 1, ro);
-    encode_grouping_launch(seg, s, gr, lc);
+    encode_route_launch(seg, s, 1, ro, gr.hist);
+    encode_grouping_launch(seg, s, gr, lc, true);
 }
 }  // namespace
 
