@@ -28,7 +28,8 @@ constexpr uint32_t kCounterWords = 8;
 static_assert(sizeof(Plan) <= kCounterBytes && kCounterBytes + 2 * 4 * kCounterWords <= kPlanSlotBytes,
               "counters in the plan slot's padding");
 // The grouping's column-scan workgroups count themselves in at this word of the slot (the
-// count kernel zeroes it; the plan fill that follows leaves it zero).
+// count kernel zeroes it, or in a route/gather composition the router; the plan fill that
+// follows leaves it zero).
 constexpr uint32_t kArriveBytes = kCounterBytes + 2 * 4 * kCounterWords;
 static_assert(kArriveBytes + 4 <= kPlanSlotBytes, "arrival word inside the plan slot");
 
