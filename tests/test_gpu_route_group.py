@@ -116,6 +116,10 @@ def test_route_gather_composition(moe, layer, orc, gpu_ctx, stream, cfg_index):
     print(f"route_gather config={cfg_index}: tokens whose top-{K} differs under FP64 logits: {flips}/{T}")
     g = orc.grouping(ids_ref, E)
     n_valid = T * K - orc.plan_fields(g["plan"])["bad"]
+    # In this composition top-k counts the entries into the histogram (the router clears it)
+    # and the count kernel does not run: the per-tile counts must still be the count kernel's.
+    n_count = (T * K + 255) // 256
+    assert np.array_equal(gu.host(ws.hist, np.uint32).reshape(-1, E)[:n_count], g["hist"]), "histogram"
     assert np.array_equal(gu.host(ws.plan, np.uint8), g["plan"])
     assert np.array_equal(gu.host(ws.src, np.int32)[:n_valid], g["src"][:n_valid])
     assert np.array_equal(gu.host(ws.dst, np.int32)[:n_valid], g["dst"][:n_valid])
