@@ -77,13 +77,13 @@ def measure(moe, layer, ctx, config: int, steps: int, warmup: int, detailed: boo
     # A multi-chunk prompt runs through the chunk driver: every chunk in one segment, one set of
     # chunk scratch. The timed step encodes + validates + commits the whole prompt.
     if cfg.chunks > 1:
-        pw = layer.PromptWorkspace(ctx, cfg, inp)
+        pw = layer.PromptWorkspace(ctx, cfg, inp, guard=False)
         ws = pw.chunk
 
         def encode(seg):
             return pw.encode(seg)
     else:
-        ws = layer.LayerWorkspace(ctx, cfg, inp)
+        ws = layer.LayerWorkspace(ctx, cfg, inp, guard=False)
         lb = ws.layer_buffers()
 
         def encode(seg):
@@ -182,7 +182,7 @@ def measure_route(moe, layer, ctx, steps: int):
     T, d, E, K = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k
     N = T * K
     log("config 1 (route_group): generating inputs")
-    ws = layer.LayerWorkspace(ctx, cfg, layer.make_inputs(cfg, with_experts=False))
+    ws = layer.LayerWorkspace(ctx, cfg, layer.make_inputs(cfg, with_experts=False), guard=False)
     sh = torch.cuda.current_stream().cuda_stream
     rg = ws.route_gather_buffers()
     acc = {}
@@ -223,7 +223,7 @@ def measure_decode(moe, layer, ctx, name: str, steps: int, inputs=None):
     T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
     N = T * K
     inp = inputs if inputs is not None else layer.make_inputs(cfg)
-    ws = layer.DecodeWorkspace(ctx, cfg, inp)
+    ws = layer.DecodeWorkspace(ctx, cfg, inp, guard=False)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
     lb = ws.layer_buffers()

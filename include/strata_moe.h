@@ -112,7 +112,10 @@ sm_status sm_buffer_unregister(sm_context* ctx, uint64_t handle);
 
 sm_status sm_segment_begin(sm_context* ctx, sm_segment** out);
 /* Launches every recorded step in order on `hip_stream` (a hipStream_t; NULL = default
- * stream) and frees the segment. Refused (and the segment freed) if any encode failed. */
+ * stream) and frees the segment. Refused (and the segment freed) if any encode failed, and
+ * with SM_E_ARGUMENT (nothing launched) if `hip_stream` is capturing a graph: the expert
+ * address tables are copied from the context's reusable pinned host ring when the launches
+ * run, so a captured graph would replay whatever tables a later commit left there. */
 sm_status sm_segment_commit(sm_segment* seg, void* hip_stream);
 /* Measurement form of sm_segment_commit (no counterpart in the reference, whose command
  * buffers report GPU start/end times instead): brackets every launch with HIP events on
@@ -485,8 +488,10 @@ sm_status sm_submit_full_layer(sm_context* ctx, void* stream, const sm_moe_shape
                                char* err, size_t cap);
 /* The full-mode layer (as sm_submit_full_layer) with its workspace in the library's fixed
  * per-GPU scratch instead of caller views. No counterpart in the reference: it is for callers
- * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc); it allocates nothing. b->route_gather.histogram,
+ * that cannot allocate device memory (tight serving loops, harnesses that forbid hipMalloc); it
+ * allocates nothing. Like every commit it refuses a capturing stream (SM_E_ARGUMENT): the expert
+ * address tables are copied from the context's reusable pinned host ring when the launches run,
+ * so a captured graph would replay stale tables. b->route_gather.histogram,
  * b->gate_up.weights.address_snapshot and b->down.weights.address_snapshot must be null views:
  * the histogram ((ceil(T*k/256) + 1) * E * 4 bytes, at most SM_FIXED_SCRATCH_HISTOGRAM_BYTES,
  * else SM_E_SHAPE) and both snapshots live in the scratch. Every call on a GPU uses that GPU's
@@ -574,11 +579,23 @@ int sm_lease_set_pins(const sm_lease_set* leases, uint32_t layer, uint64_t addre
  * `plan` is committed on it), retires the lease set's pins of earlier layers, reads the plan
  * (only the header when skip is set; n_miss must match the groups marked non-resident), resolves
  * every non-resident group's expert into a slot and writes its three slot addresses into
- * table[(layer * E + e) * 3 + role] (n_table >= (layer + 1) * E * 3). On failure nothing of the
- * layer is pinned and the table row may be partly written. */
+ * table[(layer * E + e) * 3 + role] (n_table >= (layer + 1) * E * 3). Misses are read from the
+ * file by up to 8 host threads (kExpertFetchWorkers, experts.hpp:14) and copied into their slots
+ * asynchronously on `stream`: the expert segment must be committed on `stream` (or on a stream
+ * that waits for it). On failure nothing of the layer is pinned, the slots it was filling are
+ * emptied and the table row may be partly written. */
 sm_status sm_expert_store_resolve_layer(sm_expert_store* store, void* stream, uint32_t layer, sm_view plan,
                                         sm_lease_set* leases, uint64_t* table, uint64_t n_table,
                                         sm_store_stats* stats, char* err, size_t cap);
+/* prefetch_layer / prefetch_experts (experts.hpp:90-94): warms experts of `layer` into slots of
+ * half layer % 2 ahead of its plan, so that a later resolve of the layer finds them cached
+ * (stats.hits). experts: n_experts expert ids, or NULL for every expert of the layer in id
+ * order. Cached experts count as hits; the others are read as in resolve and copied
+ * asynchronously on `stream` into free or least recently used unpinned slots, never evicting a
+ * slot this call filled, and the call stops (successfully) when no such slot is left. Pins
+ * nothing. */
+sm_status sm_expert_store_prefetch(sm_expert_store* store, void* stream, uint32_t layer, const int32_t* experts,
+                                   uint32_t n_experts, sm_store_stats* stats, char* err, size_t cap);
 
 /* ---- after completion ----------------------------------------------------------------- */
 /* Synchronises `stream`, then reads the plan's `bad` count and up to two status words

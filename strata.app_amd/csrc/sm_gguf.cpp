@@ -362,6 +362,21 @@ sm_status sm_gguf_expert_layout(const sm_gguf* g, uint32_t n_layers, sm_expert_l
 sm_status sm_gguf_load_experts(sm_gguf* g, sm_context* ctx, void* stream, const sm_expert_layout* L, sm_view storage,
                                uint64_t* addresses, uint64_t n_addresses, char* err, size_t cap) {
     if (!g || !ctx || !L || !addresses) return fail(err, cap, SM_E_ARGUMENT, "GGUF load arguments are null");
+    // The caller's layout is a plain struct: it must be the one this file gives for its layer
+    // count (an edited layout, or one made from another file, could place a tensor past the
+    // storage or name a tensor the file lacks). Everything below uses the recomputed one.
+    if (L->n_layers == 0 || L->n_layers > SM_GGUF_MAX_LAYERS)
+        return fail(err, cap, SM_E_ARGUMENT, "expert layout needs 1..SM_GGUF_MAX_LAYERS layers");
+    sm_expert_layout mine{};
+    char why[256] = {0};
+    if (sm_gguf_expert_layout(g, L->n_layers, &mine, why, sizeof why) != SM_OK)
+        return fail(err, cap, SM_E_ARGUMENT, std::string("expert layout does not fit this GGUF file: ") + why);
+    bool same = L->n_experts == mine.n_experts && L->hidden == mine.hidden && L->expert_ff == mine.expert_ff &&
+                L->gate_up == mine.gate_up && L->down == mine.down && L->total_bytes == mine.total_bytes;
+    for (uint32_t l = 0; l < mine.n_layers && same; ++l)
+        for (int r = 0; r < 3; ++r) same = same && L->offsets[l][r] == mine.offsets[l][r];
+    if (!same) return fail(err, cap, SM_E_ARGUMENT, "expert layout does not match this GGUF file");
+    L = &mine;
     const uint64_t E = L->n_experts;
     uint64_t need_words = 0;
     if (!mul_ok2(uint64_t(L->n_layers) * E, 3, need_words) || n_addresses < need_words)
@@ -371,6 +386,7 @@ sm_status sm_gguf_load_experts(sm_gguf* g, sm_context* ctx, void* stream, const 
     if (vs != SM_OK)
         return fail(err, cap, vs, vs == SM_E_OWNERSHIP ? "expert storage view is not owned by this context"
                                                        : "expert storage view is undersized or misaligned");
+    if (sm_internal_make_current(ctx) != SM_OK) return fail(err, cap, SM_E_DEVICE, "the context's device cannot be made current");
     const char* roles[3] = {"gate", "up", "down"};
     // Pinned staging: two chunks, each copied while the other is read from the file.
     constexpr uint64_t kChunk = 16ull << 20;
@@ -387,7 +403,8 @@ sm_status sm_gguf_load_experts(sm_gguf* g, sm_context* ctx, void* stream, const 
     uint64_t k = 0;  // chunk counter
     for (uint32_t l = 0; l < L->n_layers && st == SM_OK; ++l) {
         for (int r = 0; r < 3 && st == SM_OK; ++r) {
-            const auto& t = g->tensors[g->index.at(layer_name(l, roles[r]))];
+            const auto it = g->index.find(layer_name(l, roles[r]));  // present: the layout found it
+            const auto& t = g->tensors[it->second];
             const uint64_t dst = base + L->offsets[l][r];
             for (uint64_t off = 0; off < t.bytes && st == SM_OK; off += kChunk, ++k) {
                 const int b = int(k & 1);

@@ -802,6 +802,11 @@ extern "C" {
 
 uint32_t sm_abi_version(void) { return SM_ABI_VERSION; }
 
+sm_status sm_internal_make_current(sm_context* ctx) {
+    if (!ctx || !ctx->has_device || hipSetDevice(ctx->device) != hipSuccess) return SM_E_DEVICE;
+    return SM_OK;
+}
+
 sm_status sm_internal_resolve_view(sm_context* ctx, sm_view v, uint64_t need, uint64_t align, uintptr_t* out) {
     if (!ctx || !out || align == 0) return SM_E_ARGUMENT;
     sm_context::Alloc a{};
@@ -915,6 +920,13 @@ sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
     sm_status st = SM_OK;
     sm_context* ctx = seg->ctx;
     if (!ctx->has_device || hipSetDevice(ctx->device) != hipSuccess) st = SM_E_DEVICE;
+    // The expert address tables reach the GPU from the context's pinned host ring, whose slots
+    // are reused once the launch that read them has run. A captured graph would copy from its
+    // slot again at every replay, after later commits rewrote it, so no segment runs on a
+    // stream that is capturing.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (st == SM_OK && (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone))
+        st = SM_E_ARGUMENT;
     bool use_side = false;
     for (const auto& step : seg->steps) use_side = use_side || (step.side && ev == nullptr);
     std::unique_lock<std::mutex> side_lk(ctx->side_mu, std::defer_lock);
@@ -1389,6 +1401,15 @@ sm_status sm_encode_prefill_moe_chunks(sm_segment* seg, const sm_chunk_schedule*
 
 // ---- standalone transactional forms --------------------------------------------------
 
+// What a failed commit reports (empty on success).
+static const char* commit_message(sm_status st) {
+    if (st == SM_OK) return "";
+    if (st == SM_E_ARGUMENT)
+        return "segment committed on a capturing stream: the expert address tables are read from the "
+               "context's reusable host ring when the launches run, so segments run outside stream capture";
+    return "HIP launch failed";
+}
+
 #define SM_SUBMIT_BODY(ENCODE_CALL)                                                   \
     sm_segment* seg = nullptr;                                                        \
     sm_status st = sm_segment_begin(ctx, &seg);                                       \
@@ -1400,8 +1421,7 @@ sm_status sm_encode_prefill_moe_chunks(sm_segment* seg, const sm_chunk_schedule*
         return st;                                                                    \
     }                                                                                 \
     st = sm_segment_commit(seg, stream);                                              \
-    if (st != SM_OK && err && cap) std::snprintf(err, cap, "HIP launch failed");      \
-    else if (err && cap) err[0] = 0;                                                  \
+    if (err && cap) std::snprintf(err, cap, "%s", commit_message(st));                \
     return st;
 
 sm_status sm_submit_route(sm_context* ctx, void* stream, const sm_moe_shape* shape, int divide,
@@ -1453,6 +1473,14 @@ sm_status sm_submit_full_layer_fixed_scratch(sm_context* ctx, void* stream, cons
         if (err && cap) std::snprintf(err, cap, "%s", msg);
     };
     if (ctx == nullptr) return SM_E_ARGUMENT;
+    // Checked before anything is encoded (no ring slot is claimed): see run_segment.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (ctx->has_device && hipSetDevice(ctx->device) == hipSuccess &&
+        hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &capture) == hipSuccess &&
+        capture != hipStreamCaptureStatusNone) {
+        message(commit_message(SM_E_ARGUMENT));
+        return SM_E_ARGUMENT;
+    }
     FixedScratch fs;
     if (ctx->fixed_scratch != 0) {
         fs.hist = ctx->fixed_scratch;
@@ -1474,7 +1502,7 @@ sm_status sm_submit_full_layer_fixed_scratch(sm_context* ctx, void* stream, cons
         return SM_E_DEVICE;
     }
     st = sm_segment_commit(seg, stream);
-    message(st != SM_OK ? "HIP launch failed" : "");
+    message(commit_message(st));
     return st;
 }
 

@@ -113,11 +113,44 @@ def _dev(a: np.ndarray, device):
     return torch.from_numpy(np.ascontiguousarray(a)).to(device)
 
 
+GUARD_BYTES = 4096
+GUARD_FILL = 0xA5
+
+
+class _Guarded:
+    """Allocates output buffers; with `on`, each is the interior of a larger allocation with
+    GUARD_BYTES of GUARD_FILL on both sides (only the interior is registered), so a write past
+    either end shows up in bad()."""
+
+    def __init__(self, dev, on: bool):
+        self.dev, self.on, self.wholes = dev, on, []
+
+    def empty(self, nbytes: int, dtype):
+        import torch
+        if not self.on:
+            return torch.empty(nbytes // torch.tensor([], dtype=dtype).element_size(), dtype=dtype, device=self.dev)
+        whole = torch.full((nbytes + 2 * GUARD_BYTES,), GUARD_FILL, dtype=torch.uint8, device=self.dev)
+        self.wholes.append(whole)
+        return whole[GUARD_BYTES:GUARD_BYTES + nbytes].view(dtype)
+
+    def bad(self) -> list:
+        """Indices (allocation order) of the buffers whose guard bytes changed."""
+        out = []
+        for i, whole in enumerate(self.wholes):
+            if not (bool((whole[:GUARD_BYTES] == GUARD_FILL).all()) and bool((whole[-GUARD_BYTES:] == GUARD_FILL).all())):
+                out.append(i)
+        return out
+
+
 class LayerWorkspace:
-    """Device buffers and C-ABI structs of one layer call (one chunk of `cfg.rows` tokens)."""
+    """Device buffers and C-ABI structs of one layer call (one chunk of `cfg.rows` tokens).
+
+    guard: every buffer the layer writes is the interior of a larger allocation with
+    GUARD_BYTES of GUARD_FILL on both sides (the registered buffer is the interior only), so a
+    write past either end of an output shows up in check_guards()."""
 
     def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0",
-                 chunk: int = 0):
+                 chunk: int = 0, guard: bool = True):
         import torch
         self.ctx, self.cfg, self.inputs = ctx, cfg, inputs
         T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
@@ -125,9 +158,10 @@ class LayerWorkspace:
         shape = cfg.shape()
         self.shape = shape
         dev = torch.device(device)
+        self._guards = _Guarded(dev, guard)
 
         def empty(nbytes, dtype=torch.uint8):
-            return torch.empty(nbytes // torch.tensor([], dtype=dtype).element_size(), dtype=dtype, device=dev)
+            return self._guards.empty(nbytes, dtype)
 
         reg = ctx.register
         self.x = reg(_dev(inputs.x[chunk * T:(chunk + 1) * T].view(np.uint16).view(np.int16), dev))
@@ -144,7 +178,7 @@ class LayerWorkspace:
         self.xs = reg(empty(N * d * 2, torch.int16))
         self.hidden = reg(empty(N * I * 2, torch.int16))
         self.parts = reg(empty(N * d * 4, torch.float32))
-        self.status = reg(torch.zeros(4, dtype=torch.int32, device=dev))   # [gate/up, down, -, -]
+        self.status = reg(empty(16, torch.int32).zero_())   # [gate/up, down, -, -]
         self.snap_gu = reg(empty(E * 3 * 8, torch.int64))
         self.snap_dn = reg(empty(E * 3 * 8, torch.int64))
         self.out = reg(empty(T * d * 4, torch.float32))
@@ -169,6 +203,10 @@ class LayerWorkspace:
             self.sh_out = reg(empty(T * d * 4, torch.float32))
             self.sh_gl = reg(empty(T * 4, torch.float32))
         self.formats = moe.LayerFormats(cfg.gate_up_fmt, cfg.down_fmt, cfg.shared_fmt)
+
+    def check_guards(self) -> list:
+        """Indices (allocation order) of the output buffers whose guards were written."""
+        return self._guards.bad()
 
     # ---- per-stage buffer structs ----
     def route_gather_buffers(self) -> moe.RouteGatherBuffers:
@@ -231,14 +269,15 @@ class PromptWorkspace:
     rows (F32), and one chunk's scratch (a LayerWorkspace of `cfg.rows` rows) that every chunk
     reuses. One segment runs every chunk (sm_encode_prefill_moe_chunks)."""
 
-    def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0"):
+    def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0", guard: bool = True):
         import torch
         self.ctx, self.cfg = ctx, cfg
-        self.chunk = LayerWorkspace(ctx, cfg, inputs, device, chunk=0)
+        self.chunk = LayerWorkspace(ctx, cfg, inputs, device, chunk=0, guard=guard)
         n = cfg.rows * cfg.chunks
         dev = torch.device(device)
+        self._guards = _Guarded(dev, guard)
         self.x_all = ctx.register(_dev(inputs.x.view(np.uint16).view(np.int16), dev))
-        self.out_all = ctx.register(torch.empty(n * cfg.hidden, dtype=torch.float32, device=dev))
+        self.out_all = ctx.register(self._guards.empty(n * cfg.hidden * 4, torch.float32))
         sched, err = moe.build_chunk_schedule(0, n, cfg.rows)
         if sched is None:
             raise ValueError(err)
@@ -260,6 +299,10 @@ class PromptWorkspace:
 
     def read_status(self, stream=0):
         return self.chunk.read_status(stream)
+
+    def check_guards(self) -> list:
+        """The chunk scratch's written guards, then "out_all" if the prompt output's were."""
+        return self.chunk.check_guards() + (["out_all"] if self._guards.bad() else [])
 
 
 # Decode-side layers (the Window MoE, T <= 8 rows). The first two are the reference model's own
@@ -283,16 +326,17 @@ class DecodeWorkspace:
     MoePlan (one layer), the Q8_1 input, the routed FFN's scratch, the shared expert and the
     output (sm_encode_moe_decode_layer)."""
 
-    def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0"):
+    def __init__(self, ctx: moe.Context, cfg: LayerConfig, inputs: HostInputs, device="cuda:0", guard: bool = True):
         import torch
         self.ctx, self.cfg, self.inputs = ctx, cfg, inputs
         T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
         N = T * K
         self.shape = cfg.shape()
         dev = torch.device(device)
+        self._guards = _Guarded(dev, guard)
 
         def empty(nbytes, dtype=torch.uint8):
-            return torch.empty(nbytes // torch.tensor([], dtype=dtype).element_size(), dtype=dtype, device=dev)
+            return self._guards.empty(nbytes, dtype)
 
         reg = ctx.register
         self.x = reg(_dev(inputs.x[:T].view(np.uint16).view(np.int16), dev))
@@ -308,7 +352,7 @@ class DecodeWorkspace:
         self.hidden = reg(empty(N * I * 4, torch.float32))
         self.hq = reg(empty(moe.q8_1_bytes(N, I), torch.int32))
         self.parts = reg(empty(N * d * 4, torch.float32))
-        self.status = reg(torch.zeros(1, dtype=torch.int32, device=dev))
+        self.status = reg(empty(4, torch.int32).zero_())
         self.snap_gu = reg(empty(E * 3 * 8, torch.int64))
         self.snap_dn = reg(empty(E * 3 * 8, torch.int64))
         self.out = reg(empty(T * d * 4, torch.float32))
@@ -363,6 +407,10 @@ class DecodeWorkspace:
 
     def read_status(self) -> int:
         return int(self.status.tensor.cpu().item())
+
+    def check_guards(self) -> list:
+        """Indices (allocation order) of the output buffers whose guards were written."""
+        return self._guards.bad()
 
 
 def decode_weight_bytes(cfg: LayerConfig, n_active: int) -> int:

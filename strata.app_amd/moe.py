@@ -48,7 +48,7 @@ EXPORTS = (
     "sm_gguf_open", "sm_gguf_close", "sm_gguf_tensor_count", "sm_gguf_find", "sm_gguf_expert_layout",
     "sm_gguf_load_experts", "sm_expert_slot_bytes", "sm_expert_store_create", "sm_expert_store_destroy",
     "sm_lease_set_create", "sm_lease_set_destroy", "sm_lease_set_retire_layer", "sm_lease_set_pins",
-    "sm_expert_store_resolve_layer",
+    "sm_expert_store_resolve_layer", "sm_expert_store_prefetch",
     "sm_encode_moe_plan", "sm_encode_quantize_q8_1", "sm_encode_moe_experts", "sm_encode_moe_down",
     "sm_encode_moe_swiglu", "sm_encode_moe_routed_ffn", "sm_encode_moe_combine", "sm_encode_moe_shared_ffn",
     "sm_encode_moe_decode_layer",
@@ -267,6 +267,8 @@ def library() -> C.CDLL:
         "sm_lease_set_pins": (I, [P, U32, U64, U64]),
         "sm_expert_store_resolve_layer": (I, [P, P, U32, View, P, C.POINTER(C.c_uint64), U64, C.POINTER(StoreStats),
                                               C.c_char_p, C.c_size_t]),
+        "sm_expert_store_prefetch": (I, [P, P, U32, C.POINTER(C.c_int32), U32, C.POINTER(StoreStats), C.c_char_p,
+                                         C.c_size_t]),
         "sm_build_chunk_schedule": (I, [U32, U64, U32, C.POINTER(ChunkSchedule), C.c_char_p, C.c_size_t]),
         "sm_chunk_count": (U64, [C.POINTER(ChunkSchedule)]),
         "sm_chunk_range_at": (I, [C.POINTER(ChunkSchedule), U64, C.POINTER(ChunkRange)]),
@@ -435,6 +437,18 @@ class ExpertStore:
         err = C.create_string_buffer(512)
         st = self.lib.sm_expert_store_resolve_layer(self.handle, C.c_void_p(stream), layer, plan, leases.handle,
                                                     table, len(table), C.byref(stats), err, 512)
+        if st != 0:
+            return False, f"{STATUS_NAMES.get(st, st)}: {err.value.decode()}"
+        return True, dict(hits=stats.hits, lookups=stats.lookups, file_reads=stats.file_reads,
+                          file_bytes=stats.file_bytes)
+
+    def prefetch(self, stream, layer: int, experts=None):
+        """prefetch_layer (experts None) / prefetch_experts: (True, stats) or (False, message)."""
+        stats = StoreStats()
+        err = C.create_string_buffer(512)
+        ids = None if experts is None else (C.c_int32 * len(experts))(*experts)
+        n = 0 if experts is None else len(experts)
+        st = self.lib.sm_expert_store_prefetch(self.handle, C.c_void_p(stream), layer, ids, n, C.byref(stats), err, 512)
         if st != 0:
             return False, f"{STATUS_NAMES.get(st, st)}: {err.value.decode()}"
         return True, dict(hits=stats.hits, lookups=stats.lookups, file_reads=stats.file_reads,

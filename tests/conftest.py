@@ -44,3 +44,36 @@ def gpu_ctx(moe):
 def stream():
     import torch
     return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.fixture(autouse=True)
+def _output_guards(request):
+    """Every workspace a GPU test makes allocates its outputs between guard regions (4 KiB of a
+    fill byte on both sides, outside the registered buffer: the reference's poison guards,
+    tests/metal/twin.hpp:42-66). After the test, each workspace's guards must be untouched."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    lay = ge.load_package().layer
+    classes = (lay.LayerWorkspace, lay.PromptWorkspace, lay.DecodeWorkspace)
+    originals = {c: c.__init__ for c in classes}
+    made = []
+
+    def wrap(orig):
+        def init(self, *a, **k):
+            orig(self, *a, **k)
+            made.append(self)
+        return init
+
+    for c in classes:
+        c.__init__ = wrap(originals[c])
+    try:
+        yield
+    finally:
+        for c in classes:
+            c.__init__ = originals[c]
+    import torch
+    torch.cuda.synchronize()
+    for ws in made:
+        bad = ws.check_guards()
+        assert not bad, f"{type(ws).__name__} {ws.cfg.name}: guard bytes written around output buffers {bad}"

@@ -4,8 +4,10 @@ CPU: the GGUF directory parse and the expert layout against what the writer reco
 rejections (bad magic and version, truncated file, data outside the file or off the alignment,
 duplicate tensors, a missing or misshapen expert tensor, gate/up of different types, a
 non-block expert type), following the reference's layout checks (src/metal/engine/window.cpp:
-34-56,128-270). GPU: the experts loaded from a file drive a full layer whose output equals, bit
-for bit, the same layer on weights uploaded directly.
+34-56,128-270). GPU: the device storage equals the file's tensor bytes and the table points at
+every expert; the experts loaded from a file drive a full layer checked stage by stage against
+the CPU oracle on the file's bytes, and equal, bit for bit, the same layer on the same bytes
+uploaded directly.
 """
 import numpy as np
 import pytest
@@ -95,30 +97,97 @@ def test_layout_rejections(tmp_path, moe, fn, msg):
     assert L is None and msg in err, err
 
 
-@pytest.mark.gpu
-def test_layer_on_experts_loaded_from_file(tmp_path, moe, layer, gpu_ctx, stream):
-    """Layer 1's experts loaded from a GGUF file into one device allocation, selected through the
-    [layer][E][3] table, give the same layer output as the same bytes uploaded directly."""
-    import torch
-    print("case layer on GGUF experts", flush=True)
-    p, _, experts = _write(tmp_path, moe, n_layers=2, E=16, d=256, I=128)
+def test_load_rejects_a_layout_the_file_does_not_give(tmp_path, moe):
+    """The layout the caller passes must be the one this file gives for its layer count: an
+    edited offset or size, a layer count past the file or the bound, or a layout from another
+    file is refused before anything is read or copied (SM_E_ARGUMENT)."""
+    from test_abi_host import Fake
+    p, _, _ = _write(tmp_path, moe, n_layers=2, E=16, d=256, I=128)
     f = moe.GgufFile(p)
-    assert f, f.error
     L, err = f.expert_layout(2)
     assert L is not None, err
+    p2, _, _ = _write(tmp_path, moe, name="other.gguf", n_layers=2, E=8, d=256, I=128)
+    L_other, err = moe.GgufFile(p2).expert_layout(2)
+    assert L_other is not None, err
+    fake = Fake(moe)
+    storage = fake.buf(L.total_bytes + (1 << 20))
+
+    def edited(fn):
+        c = moe.ExpertLayout.from_buffer_copy(L)
+        fn(c)
+        return c
+
+    def more_layers(c):
+        c.n_layers = 3
+
+    def too_many(c):
+        c.n_layers = 65
+
+    def offset(c):
+        c.offsets[1][2] += 256
+
+    def total(c):
+        c.total_bytes -= 256
+
+    def fmt(c):
+        c.down = moe.Q4_K
+
+    cases = [(edited(more_layers), "does not fit this GGUF file"), (edited(too_many), "1..SM_GGUF_MAX_LAYERS"),
+             (edited(offset), "does not match"), (edited(total), "does not match"), (edited(fmt), "does not match"),
+             (L_other, "does not match")]
+    for bad, msg in cases:
+        with pytest.raises(RuntimeError, match="SM_E_ARGUMENT") as ex:
+            f.load_experts(fake.ctx, 0, bad, storage.view())
+        assert msg in str(ex.value), str(ex.value)
+
+
+@pytest.mark.gpu
+def test_layer_on_experts_loaded_from_file(tmp_path, moe, layer, orc, gpu_ctx, stream):
+    """Every expert tensor of both layers lands in device storage byte for byte as the file holds
+    it, and the [layer][E][3] table points at each expert's slab. Layer 1's experts, selected
+    through the table, drive a full layer whose stages match the CPU oracle run on the file's
+    own bytes at every grouped entry and token, and whose output equals, bit for bit, the same
+    layer on the same bytes uploaded directly."""
+    import torch
+    from test_gpu_layer import _check_stages
+    print("case layer on GGUF experts", flush=True)
+    E, n_layers = 16, 2
+    p, _, experts = _write(tmp_path, moe, n_layers=n_layers, E=E, d=256, I=128)
+    f = moe.GgufFile(p)
+    assert f, f.error
+    L, err = f.expert_layout(n_layers)
+    assert L is not None, err
     storage = gpu_ctx.register(torch.empty(L.total_bytes, dtype=torch.uint8, device="cuda"))
+    storage.tensor.fill_(0x5A)
     table = f.load_experts(gpu_ctx, stream, L, storage.view())
-    cfg = layer.LayerConfig("gguf", 128, 256, 16, 4, 128, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=5)
+    torch.cuda.synchronize()
+    dev = storage.tensor.cpu().numpy()
+    raw = p.read_bytes()
+    file_w = {}
+    for l in range(n_layers):
+        for r, nm in enumerate(("gate", "up", "down")):
+            t = f.find(f"blk.{l}.ffn_{nm}_exps.weight")
+            want = np.frombuffer(raw, np.uint8, count=t["bytes"], offset=t["offset"])
+            assert want.tobytes() == experts[l][r].tobytes(), f"file bytes of layer {l} {nm}"
+            got = dev[L.offsets[l][r]:L.offsets[l][r] + t["bytes"]]
+            assert np.array_equal(got, want), f"device storage of layer {l} {nm} differs from the file"
+            slab = t["bytes"] // E
+            for e in range(E):
+                assert table[(l * E + e) * 3 + r] == storage.ptr + L.offsets[l][r] + e * slab
+            file_w[l, r] = want.copy()
+    cfg = layer.LayerConfig("gguf", 128, 256, E, 4, 128, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=5)
     inp = layer.make_inputs(cfg)
-    inp.w_gate, inp.w_up, inp.w_down = experts[1]
+    inp.w_gate, inp.w_up, inp.w_down = file_w[1, 0], file_w[1, 1], file_w[1, 2]
     ws = layer.LayerWorkspace(gpu_ctx, cfg, inp)
+    ws.gu_table = moe.ExpertTable(table, ws.snap_gu.view(), [storage.view()], n_layers=n_layers, layer=1)
+    ws.dn_table = moe.ExpertTable(table, ws.snap_dn.view(), [storage.view()], n_layers=n_layers, layer=1)
+    for n in ("hidden", "parts", "out"):
+        getattr(ws, n).tensor.view(torch.uint8).fill_(0x7F)
     ws.run_layer(stream)
     assert ws.read_status(stream) == (0, 0, 0)
-    ref = ws.out.tensor.cpu().numpy().copy()
-    assert table[(1 * 16 + 3) * 3 + 2] == storage.ptr + L.offsets[1][2] + 3 * 256 * 4 * 34
-    ws.gu_table = moe.ExpertTable(table, ws.snap_gu.view(), [storage.view()], n_layers=2, layer=1)
-    ws.dn_table = moe.ExpertTable(table, ws.snap_dn.view(), [storage.view()], n_layers=2, layer=1)
-    ws.out.tensor.fill_(float("nan"))
-    ws.run_layer(stream)
-    assert ws.read_status(stream) == (0, 0, 0)
-    assert np.array_equal(ws.out.tensor.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    _check_stages(moe, layer, orc, ws, inp, cfg, n_sample_tokens=None, every_entry=True)
+    loaded = ws.out.tensor.cpu().numpy().copy()
+    direct = layer.LayerWorkspace(gpu_ctx, cfg, inp)
+    direct.run_layer(stream)
+    assert direct.read_status(stream) == (0, 0, 0)
+    assert np.array_equal(direct.out.tensor.cpu().numpy().view(np.uint32), loaded.view(np.uint32))

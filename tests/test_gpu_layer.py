@@ -33,10 +33,13 @@ def boundary_entries(plan_fields) -> np.ndarray:
     return np.unique(np.asarray(sel, np.int64))
 
 
-def _check_stages(moe, layer, orc, ws, inp, cfg, chunk=0, n_sample_tokens=48, every_entry=False):
+def _check_stages(moe, layer, orc, ws, inp, cfg, chunk=0, n_sample_tokens=48, every_entry=False,
+                  residency_marks=False):
     """Checks one layer call's outputs (already computed in `ws`): the expert products at the
     boundary entries (or at every entry), combine on every token, the layer on sampled tokens
-    (n_sample_tokens None: every token). Returns the grouped entries checked."""
+    (n_sample_tokens None: every token). residency_marks: the plan was built with residency
+    marks (tiered experts), so its n_miss, skip and grp_res fields are left out of the plan
+    comparison. Returns the grouped entries checked."""
     T, d, E, K, I, Is = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff, cfg.shared_ff
     N = T * K
     x = inp.x[chunk * T:(chunk + 1) * T]
@@ -49,7 +52,16 @@ def _check_stages(moe, layer, orc, ws, inp, cfg, chunk=0, n_sample_tokens=48, ev
     assert np.array_equal(gu.host(ws.src, np.int32), g["src"])
     assert np.array_equal(gu.host(ws.dst, np.int32), g["dst"])
     plan = g["plan"]
-    assert np.array_equal(gu.host(ws.plan, np.uint8)[:6180], plan[:6180])
+    got_plan = gu.host(ws.plan, np.uint8)[:6180].copy()
+    if residency_marks:
+        # n_miss counts the groups marked non-resident and skip is set when there is none; the
+        # rest of the plan must equal the full-residency plan
+        words, ref_words = got_plan.view(np.int32), plan[:6180].view(np.int32)
+        marks = words[520:520 + words[0]]
+        assert words[2] == int((marks == 0).sum()) and words[3] == int(words[2] == 0)
+        words[2:4] = ref_words[2:4]                  # n_miss, skip
+        words[520:1032] = ref_words[520:1032]        # grp_res
+    assert np.array_equal(got_plan, plan[:6180])
     pf = orc.plan_fields(plan)
     pos = np.arange(int(pf["grp_start"][pf["n_groups"]])) if every_entry else boundary_entries(pf)
     # gathered rows: bit-exact on every entry

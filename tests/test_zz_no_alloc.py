@@ -3,7 +3,8 @@ grouping histogram and both address snapshots) lives in the library's fixed per-
 
 CPU: the entry point's own preflight (null workspace views required, the histogram bound).
 GPU: through the C ABI, two calls in a row, the second on a smaller layer, each equal bit for
-bit to the same layer run by sm_submit_full_layer with caller workspace views.
+bit to the same layer run by sm_submit_full_layer with caller workspace views; a call on a
+capturing stream is refused before anything is encoded.
 """
 import ctypes as C
 
@@ -74,3 +75,24 @@ def test_fixed_scratch_layer_matches_caller_workspace(moe, layer, gpu_ctx, strea
         for n in names:
             got = getattr(ws, n).tensor.cpu().numpy().view(np.uint8)
             assert np.array_equal(got, ref[n]), f"{cfg.name}: {n} differs from the caller-workspace layer"
+
+
+@pytest.mark.gpu
+def test_fixed_scratch_refuses_a_capturing_stream(moe, layer, gpu_ctx):
+    """Under stream capture the entry point returns SM_E_ARGUMENT before encoding anything (its
+    expert address tables would be replayed from a reusable host slot), so the capture holds
+    no launch and the outputs stay as they were."""
+    import torch
+    print("case fixed scratch under capture", flush=True)
+    cfg = layer.LayerConfig("fixed_capture", 64, 256, 16, 4, 128, 0, moe.Q8_0, moe.Q8_0, moe.F16, seed=93)
+    ws = layer.LayerWorkspace(gpu_ctx, cfg, layer.make_inputs(cfg))
+    lb = _fixed_views(moe, ws.layer_buffers())
+    ws.out.tensor.view(torch.uint8).fill_(0xA5)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side, capture_error_mode="thread_local"):
+        st, msg = _submit_fixed(moe, gpu_ctx, side.cuda_stream, ws.shape, ws.formats, lb)
+    assert st == SM_E_ARGUMENT and "capturing stream" in msg, (st, msg)
+    torch.cuda.synchronize()
+    assert (ws.out.tensor.view(torch.uint8).cpu().numpy() == 0xA5).all()
