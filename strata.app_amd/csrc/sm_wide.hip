@@ -1,8 +1,10 @@
 // Routed expert products for large groups on gfx950: 256-row units x 256 weight rows.
 //
-// A group with at least `wide_min` entries is cut into units of 256 consecutive grouped
-// rows (the last one partial); the 64-row tile kernels skip such groups. One unit times
-// one column tile is an item. The kernel is persistent: each workgroup (512 threads, one
+// A group with at least `wide_min` entries is cut into ceil(size / 256) units of consecutive
+// grouped rows, as even as whole 32-row blocks allow (a group of 300 rows: 160 + 140, not
+// 256 + 44); the 64-row tile kernels skip such groups. One unit times one column tile is an
+// item. A wave multiplies only the 32-row blocks of its row half that hold entries, so a unit
+// of 160 rows costs five blocks of MFMA work, not eight. The kernel is persistent: each workgroup (512 threads, one
 // per CU) walks its share of the items, so no workgroup slot is spent on idle tiles.
 //
 // Per 64-value K step, both operands sit in LDS:
@@ -13,7 +15,7 @@
 // step j. Decoding once per 256 rows, instead of once per 64-row tile, is what moves these
 // products from decode-bound to MFMA-bound.
 // Wave w multiplies rows [128 * (w >> 2), +128) by B rows of column quarter q = w & 3 with
-// 32x32x16 MFMAs: 4 row blocks x 2 column blocks of 32x32 F32 accumulators (128 VGPRs):
+// 32x32x16 MFMAs: up to 4 row blocks x 2 column blocks of 32x32 F32 accumulators (128 VGPRs):
 //   gate/up: column block 0 = gate rows [32q, +32), block 1 = the up rows [128 + 32q, +32)
 //            of the same hidden columns, so the SwiGLU epilogue pairs values of one lane;
 //   down:    output columns [64q, +64).
@@ -212,6 +214,13 @@ struct Unit {
     uint32_t a0, a1, ex;
 };
 
+// Rows per unit of a group of `size` entries: its ceil(size / 256) units are as even as whole
+// 32-row blocks allow (at most 256; every unit holds at least one row).
+__device__ __forceinline__ uint32_t unit_rows(uint32_t size) {
+    const uint32_t nu = (size + kUnitRows - 1u) / kUnitRows;
+    return 32u * ((size + 32u * nu - 1u) / (32u * nu));
+}
+
 template <int MODE>
 __device__ void zero_item(const RoutedGemm& g, const Unit& u, uint32_t ct, const int32_t* s_dst) {
     const uint32_t width = MODE == kGateUp ? 128u : 256u, c0 = ct * width, rows = u.a1 - u.a0;
@@ -327,8 +336,9 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
                 else hi_g = mid;
             }
             const uint32_t f = uint32_t(p->grp_start[lo_g]), e = uint32_t(p->grp_start[lo_g + 1]);
-            u.a0 = f + kUnitRows * (uidx - s_pref[lo_g]);
-            u.a1 = u.a0 + kUnitRows < e ? u.a0 + kUnitRows : e;
+            const uint32_t usz = unit_rows(e - f);
+            u.a0 = f + usz * (uidx - s_pref[lo_g]);
+            u.a1 = u.a0 + usz < e ? u.a0 + usz : e;
             u.ex = uint32_t(p->grp_e[lo_g]);
         }
         const uint32_t nrows = u.a1 - u.a0;
@@ -361,7 +371,10 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
             const uint32_t row = u.a0 + (R < nrows ? R : nrows - 1u);
             asrc[j] = g.a + uint64_t(row) * g.k + 8u * c;
         }
+        // Wave w copies rows [32 w, 32 w + 32): nothing for a block past the unit's rows.
+        const bool copies = 32u * wave_u < nrows;
         auto copy_a = [&](uint32_t step, uint32_t buf) {
+            if (!copies) return;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 __builtin_amdgcn_global_load_lds(
@@ -402,8 +415,11 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
         // stages nobody reads), so it has no branches and the compiler's own waits for the
         // prefetched registers count exactly the copies issued since. Rows past a partial
         // unit's end hold repeated rows; their products are dropped.
-        auto k_step = [&](uint32_t step, auto par_c) {
+        // NB: the 32-row blocks of this wave's row half that hold entries (0..4, wave-uniform);
+        // the others are neither read nor multiplied.
+        auto k_step = [&](uint32_t step, auto par_c, auto nb_c) {
             constexpr uint32_t PAR = decltype(par_c)::value;  // step & 1 == buffer index
+            constexpr int NB = decltype(nb_c)::value;
             const uint32_t last = nK - 1u;
             wait_barrier();
             prefetch(fr[PAR], step + 2u < last ? step + 2u : last);
@@ -417,9 +433,11 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
             half8 a[2][4], b[2][2];
             auto load_ops = [&](uint32_t t, int z) {
 #pragma unroll
-                for (uint32_t rb = 0; rb < 4u; ++rb) a[z][rb] = lds_ld<half8>(sa + 4096u * rb + lo[t]);
-                b[z][0] = lds_ld<half8>(sb + bofs0 + lo[t]);
-                b[z][1] = lds_ld<half8>(sb + bofs1 + lo[t]);
+                for (int rb = 0; rb < NB; ++rb) a[z][rb] = lds_ld<half8>(sa + 4096u * uint32_t(rb) + lo[t]);
+                if constexpr (NB > 0) {
+                    b[z][0] = lds_ld<half8>(sb + bofs0 + lo[t]);
+                    b[z][1] = lds_ld<half8>(sb + bofs1 + lo[t]);
+                }
             };
             // Scheduling regions (nothing moves across a sched_barrier): slice t's region holds
             // its 8 MFMAs, the operand reads of slice t + 1 and one chunk of the next step's
@@ -432,22 +450,24 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
                 const int z = int(t & 1u);
                 if (t + 1u < 4u) load_ops(t + 1u, z ^ 1);
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb)
+                for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
                     for (int cb = 0; cb < 2; ++cb)
                         acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[z][rb], b[z][cb], acc[rb][cb], 0, 0, 0);
                 if (t == 0u) fn.prepare();
                 produce(fn, nb, int(t));
-                // Two MFMAs, the next slice's reads, the other six MFMAs with the decode, then the
+                // Two MFMAs, the next slice's reads, the other MFMAs with the decode, then the
                 // chunk's LDS write: the next region's first wait then finds those reads done.
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+                if constexpr (NB > 0) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, NB + 2, 0);
 #pragma unroll
-                for (int i = 0; i < 6; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                    for (int i = 0; i < 2 * NB - 2; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
@@ -461,9 +481,22 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
         for (int s = 0; s < 4; ++s) produce(fr[0], s_b[0], s);
         compiler_fence();
         prefetch(fr[1], 1);  // nK >= 2
-        for (uint32_t step = 0; step < nK; step += 2u) {
-            k_step(step, std::integral_constant<uint32_t, 0>());
-            k_step(step + 1u, std::integral_constant<uint32_t, 1>());
+        // Blocks of this wave's row half holding entries (wave-uniform); every variant runs the
+        // same barriers, copies and decode, so the waves of the workgroup stay in step.
+        const uint32_t half_rows = nrows > 128u * rh ? nrows - 128u * rh : 0u;
+        const uint32_t nb_rows = (half_rows + 31u) / 32u;
+        auto k_loop = [&](auto nb_c) {
+            for (uint32_t step = 0; step < nK; step += 2u) {
+                k_step(step, std::integral_constant<uint32_t, 0>(), nb_c);
+                k_step(step + 1u, std::integral_constant<uint32_t, 1>(), nb_c);
+            }
+        };
+        switch (nb_rows < 4u ? nb_rows : 4u) {
+            case 0: k_loop(std::integral_constant<int, 0>()); break;
+            case 1: k_loop(std::integral_constant<int, 1>()); break;
+            case 2: k_loop(std::integral_constant<int, 2>()); break;
+            case 3: k_loop(std::integral_constant<int, 3>()); break;
+            default: k_loop(std::integral_constant<int, 4>()); break;
         }
         wait_barrier();  // the repeated copies of the last step have landed
 

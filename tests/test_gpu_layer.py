@@ -17,19 +17,28 @@ import gpu_util as gu
 
 pytestmark = pytest.mark.gpu
 
-WIDE_MIN = 128  # groups with at least this many entries run as 256-row units
+WIDE_MIN = 128  # groups with at least this many entries run as wide units
+
+
+def unit_rows(size: int) -> int:
+    """Rows per wide unit of a group: ceil(size / 256) units, as even as 32-row blocks allow."""
+    nu = -(-size // 256)
+    return 32 * -(-size // (32 * nu))
 
 
 def boundary_entries(plan_fields) -> np.ndarray:
-    """Grouped entries at both ends of every group, 64-row tile and 256-row unit."""
+    """Grouped entries at both ends of every group, 64-row tile and wide unit, and of every
+    32-row block of a wide unit (the blocks a wave multiplies)."""
     n = plan_fields["n_groups"]
     starts = plan_fields["grp_start"][: n + 1].astype(np.int64)
     sel = []
     for gi in range(n):
         f, e = int(starts[gi]), int(starts[gi + 1])
-        step = 256 if e - f >= WIDE_MIN else 64
+        step = unit_rows(e - f) if e - f >= WIDE_MIN else 64
         for u0 in range(f, e, step):
             sel += [u0, min(u0 + step, e) - 1]
+            if step != 64:
+                sel += [b for b0 in range(u0 + 32, min(u0 + step, e), 32) for b in (b0 - 1, b0)]
     return np.unique(np.asarray(sel, np.int64))
 
 
