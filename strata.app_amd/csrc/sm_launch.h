@@ -75,8 +75,10 @@ hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t top_k, ui
                            uint32_t* hist, Plan* plan, uint32_t* tiles, int32_t* src, int32_t* dst,
                            const GroupPrep* prep, const int32_t* resident, hipStream_t s,
                            bool counted = false);
-hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
-                         const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
+// The gather runs after the grouping of the same ids and histogram (it recomputes each entry's
+// grouped slot from them); d % 256 == 0.
+hipError_t launch_gather(const _Float16* x, uint32_t d, const int32_t* ids, const uint32_t* hist, uint32_t top_k,
+                         uint32_t n_experts, const Plan* plan, uint32_t n_entries, _Float16* xs, hipStream_t s);
 
 // ---- expert stage validation (the reference's plan/destination validators) ----
 // One plan check for up to two expert stages. The check's verdict goes to `status` and, when
@@ -107,11 +109,12 @@ hipError_t launch_plan_validate(const PlanCheck& c, hipStream_t s);
 // The gather of a full layer with both expert stages' checks in the same launch: one extra
 // workgroup runs the plan check `c` (its `clear` and status clearing are not used: the
 // grouping's GroupPrep zeroed both status words and the bitset `bits`), and every gather
-// workgroup marks eight entries of `dst` in `bits`, setting bit 1 of `c.status2` for an entry
+// workgroup marks its share of `dst` in `bits`, setting bit 1 of `c.status2` for an entry
 // outside [0, n_entries) or a repeated one.
-hipError_t launch_gather_checked(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
-                                 const Plan* plan, uint32_t n_entries, _Float16* xs, const PlanCheck& c,
-                                 const int32_t* dst, uint32_t* bits, hipStream_t s);
+hipError_t launch_gather_checked(const _Float16* x, uint32_t d, const int32_t* ids, const uint32_t* hist,
+                                 uint32_t top_k, uint32_t n_experts, const Plan* plan, uint32_t n_entries,
+                                 _Float16* xs, const PlanCheck& c, const int32_t* dst, uint32_t* bits,
+                                 hipStream_t s);
 // Checks that `dst` is a permutation of [0, n_entries) with a bitset (zeroed first unless
 // `bitset_clear` is false because a PlanCheck cleared it).
 hipError_t launch_destination_validate(const int32_t* dst, uint32_t* bitset, uint32_t* status,

@@ -642,31 +642,32 @@ __global__ __launch_bounds__(512) void plan_validate_kernel(PlanCheck c) {
     check_plan<512>(c, c.keep_status == 0u);
 }
 
-// Xs[a,:] = X[src[a],:] for a < the plan's valid-entry count. Workgroup b copies the rows of
-// grouped chunk b / 8 (kGatherChunk rows) whose source token lies in token slice b % 8
-// (tokens [T*s/8, T*(s+1)/8)). Every (chunk, slice) pair belongs to one workgroup, so each
-// row is written exactly once whatever the placement; workgroups are placed round-robin on
-// the 8 XCDs, so each XCD reads only its eighth of X and keeps it in its own L2 (each token
-// row is read top-k times). Wave 0 compacts the chunk's rows of its slice into LDS; the
-// workgroup then copies them kGatherRows at a time, 16 bytes per thread, each thread
-// issuing its loads for those rows before its stores. The stores are non-temporal: the
-// grouped rows are a write-once stream. The plan header is checked first as in the
-// reference's gather (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
+// Xs[a,:] = X[token(a),:] for every valid entry a < the plan's valid-entry count, walked in
+// route order. Workgroup (tile, part) takes the kCountTile route entries of histogram tile
+// `tile` and column part `part` of the rows (kGatherPart 16-byte chunks, 256 bytes). It
+// recomputes each entry's grouped slot exactly as the scatter wrote it (the tile's final
+// cursors in hist plus the entry's stable rank among the tile's equal ids), then loads each
+// token's row part once and stores it to the slots of that token's entries in the tile: X is
+// read once (a token whose entries straddle two tiles, twice), and each thread keeps its
+// token's loads ahead of a run of up to top-k stores. The stores are non-temporal: the grouped
+// rows are a write-once stream. The plan header is checked first as in the reference's gather
+// (prefill_moe.metal:282-297); an inconsistent plan writes nothing.
 // CHECK (a full layer, both expert stages on the grouping's plan): workgroup 0 runs the
-// stages' plan check (prefill_moe.metal:603-733) and the copy workgroups are 1.. (copy
-// workgroup g = b - 1 takes slice g % 8, so each XCD still reads a single slice). Copy
-// workgroup g also marks destination entries [8g, 8g + 8) in the bitset, which is the
-// reference's destination check (prefill_moe_down_dispatch.mm:470-520) spread over the
-// gather: an entry outside [0, N) or one already marked sets bit 1 of the down status.
-constexpr uint32_t kGatherChunk = 64, kGatherRows = 4;
+// stages' plan check (prefill_moe.metal:603-733) and the copy workgroups are 1..; copy
+// workgroup (tile, part) also marks its share of the tile's entries of `dst` in the bitset,
+// which is the reference's destination check (prefill_moe_down_dispatch.mm:470-520) spread
+// over the gather: an entry outside [0, N) or one already marked sets bit 1 of the down status.
+constexpr uint32_t kGatherPart = 16, kGatherBatch = 2;
 template <bool CHECK>
-__global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t rows,
-                                                     uint32_t vpr, const int32_t* __restrict__ src,
-                                                     const Plan* __restrict__ plan, uint32_t N,
+__global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x, uint32_t vpr,
+                                                     const int32_t* __restrict__ ids,
+                                                     const uint32_t* __restrict__ hist, uint32_t K, uint32_t E,
+                                                     uint32_t parts, const Plan* __restrict__ plan, uint32_t N,
                                                      u32x4* __restrict__ xs, PlanCheck c,
                                                      const int32_t* __restrict__ dst, uint32_t* __restrict__ bits) {
-    static_assert(kGatherChunk == 64, "one wave compacts a chunk");
-    __shared__ uint32_t s_row[kGatherChunk], s_tok[kGatherChunk], s_n;
+    __shared__ uint32_t wcnt[4][512];
+    __shared__ uint32_t s_base[512];
+    __shared__ uint32_t s_slot[kCountTile];
     uint32_t b = blockIdx.x;
     if constexpr (CHECK) {
         if (b == 0) {
@@ -675,13 +676,30 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
         }
         b -= 1u;
     }
-    const uint32_t tid = threadIdx.x, slice = b & 7u, a = (b >> 3) * kGatherChunk + tid;
-    const uint32_t t_lo = uint32_t((uint64_t(rows) * slice) >> 3);
-    const uint32_t t_hi = uint32_t((uint64_t(rows) * (slice + 1u)) >> 3);
-    const int32_t sv = tid < kGatherChunk && a < N ? src[a] : -1;  // issued before the plan reads
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tile = b / parts, part = b - tile * parts;
+    const uint32_t i0 = tile * kCountTile, i1 = i0 + kCountTile < N ? i0 + kCountTile : N;
+    // Thread (row lane j, chunk) copies tokens t0 + j, t0 + j + rpar, ... of the tile; the first
+    // kGatherBatch of them are loaded before anything else (they depend on the tile alone).
+    const uint32_t rpar = 256u / kGatherPart, j = tid / kGatherPart;
+    const uint32_t col = part * kGatherPart + (tid - j * kGatherPart);
+    const uint32_t t0 = i0 / K, t1 = (i1 - 1u) / K;
+    u32x4 v[kGatherBatch];
+    auto load_batch = [&](uint32_t tb) {
+#pragma unroll
+        for (uint32_t q = 0; q < kGatherBatch; ++q) {
+            const uint32_t t = tb + j + q * rpar;
+            if (t <= t1) v[q] = x[uint64_t(t) * vpr + col];
+        }
+    };
+    load_batch(t0);
+    const uint64_t entry = uint64_t(i0) + tid;
+    const int32_t id = entry < N ? ids[entry] : -1;  // issued before the plan reads
+    for (uint32_t e = tid; e < E; e += 256u) s_base[e] = hist[uint64_t(tile) * E + e];
     if constexpr (CHECK) {
-        const uint32_t i = b * 8u + (tid - 192u);  // wave 3; wave 0 compacts
-        if (tid >= 192u && tid < 200u && i < N) {
+        const uint32_t per = (kCountTile + parts - 1u) / parts;
+        const uint32_t i = i0 + part * per + tid;
+        if (tid < per && i < i1) {
             const uint32_t dv = uint32_t(dst[i]);
             if (dv >= N) {
                 atomicOr(c.status2, 2u);
@@ -691,33 +709,49 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
             }
         }
     }
+    for (uint32_t k = tid; k < 4u * 512u; k += 256u) (&wcnt[0][0])[k] = 0u;
     const uint32_t ng = plan->n_groups;
     if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) return;
     const int32_t sorted_signed = plan->grp_start[ng];
     if (sorted_signed < 0 || uint32_t(sorted_signed) != N - plan->bad) return;
-    const uint32_t sorted = uint32_t(sorted_signed);
-    if (tid < kGatherChunk) {
-        const bool mine = a < sorted && sv >= 0 && uint32_t(sv) >= t_lo && uint32_t(sv) < t_hi;
-        const uint64_t m = __ballot(mine);
-        if (mine) {
-            const uint32_t pos = uint32_t(__popcll(m & ((1ull << tid) - 1ull)));
-            s_row[pos] = a;
-            s_tok[pos] = uint32_t(sv);
-        }
-        if (tid == 0) s_n = uint32_t(__popcll(m));
+    // The entry's slot, as group_scatter_kernel computed it.
+    const bool valid = id >= 0 && uint32_t(id) < E;
+    const uint32_t key = valid ? uint32_t(id) : 1023u;
+    uint64_t match = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 10; ++bit) {
+        const bool on = (key >> bit) & 1u;
+        const uint64_t bal = __ballot(on);
+        match &= on ? bal : ~bal;
     }
+    const uint32_t rank = __popcll(match & ((1ull << lane) - 1ull));
+    const uint64_t gt = lane == 63u ? 0ull : (~0ull << (lane + 1u));
     __syncthreads();
-    const uint32_t n = s_n;
-    for (uint32_t i = 0; i < n; i += kGatherRows)
-        for (uint32_t c = tid; c < vpr; c += 256u) {
-            u32x4 v[kGatherRows];
+    if (valid && (match & gt) == 0ull) wcnt[wave][id] = rank + 1u;
+    __syncthreads();
+    uint32_t slot = ~0u;
+    if (valid) {
+        slot = s_base[id] + rank;
+        for (uint32_t w = 0; w < wave; ++w) slot += wcnt[w][id];
+        if (slot >= uint32_t(sorted_signed)) slot = ~0u;  // only behind an inconsistent histogram
+    }
+    s_slot[tid] = slot;
+    __syncthreads();
+    for (uint32_t tb = t0;; tb += kGatherBatch * rpar) {
+        if (tb != t0) load_batch(tb);
 #pragma unroll
-            for (uint32_t r = 0; r < kGatherRows; ++r)
-                if (i + r < n) v[r] = x[uint64_t(s_tok[i + r]) * vpr + c];
-#pragma unroll
-            for (uint32_t r = 0; r < kGatherRows; ++r)
-                if (i + r < n) __builtin_nontemporal_store(v[r], &xs[uint64_t(s_row[i + r]) * vpr + c]);
+        for (uint32_t q = 0; q < kGatherBatch; ++q) {
+            const uint32_t t = tb + j + q * rpar;
+            if (t > t1) break;
+            const uint32_t r0 = t * K < i0 ? i0 - t * K : 0u;
+            const uint32_t r1 = t * K + K > i1 ? i1 - t * K : K;
+            for (uint32_t r = r0; r < r1; ++r) {
+                const uint32_t sl = s_slot[t * K + r - i0];
+                if (sl != ~0u) __builtin_nontemporal_store(v[q], &xs[uint64_t(sl) * vpr + col]);
+            }
         }
+        if (tb + kGatherBatch * rpar > t1) break;
+    }
 }
 
 __global__ __launch_bounds__(256) void bitset_clear_kernel(uint32_t* __restrict__ bits, uint32_t words) {
@@ -782,23 +816,23 @@ hipError_t launch_grouping(const int32_t* ids, uint32_t rows, uint32_t K, uint32
     return hipGetLastError();
 }
 
-hipError_t launch_gather(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
-                         const Plan* plan, uint32_t N, _Float16* xs, hipStream_t s) {
-    const uint32_t vpr = d / 8;
-    const uint32_t blocks = 8u * ((N + kGatherChunk - 1) / kGatherChunk);  // (chunk, token slice) pairs
-    gather_kernel<false><<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
-                                                reinterpret_cast<u32x4*>(xs), PlanCheck{}, nullptr, nullptr);
+hipError_t launch_gather(const _Float16* x, uint32_t d, const int32_t* ids, const uint32_t* hist, uint32_t K,
+                         uint32_t E, const Plan* plan, uint32_t N, _Float16* xs, hipStream_t s) {
+    const uint32_t vpr = d / 8, parts = vpr / kGatherPart;  // d % 256 == 0
+    const uint32_t blocks = parts * ((N + kCountTile - 1) / kCountTile);  // (tile, part) pairs
+    gather_kernel<false><<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), vpr, ids, hist, K, E, parts,
+                                                plan, N, reinterpret_cast<u32x4*>(xs), PlanCheck{}, nullptr, nullptr);
     return hipGetLastError();
 }
 
-hipError_t launch_gather_checked(const _Float16* x, uint32_t rows, uint32_t d, const int32_t* src,
-                                 const Plan* plan, uint32_t N, _Float16* xs, const PlanCheck& c,
+hipError_t launch_gather_checked(const _Float16* x, uint32_t d, const int32_t* ids, const uint32_t* hist, uint32_t K,
+                                 uint32_t E, const Plan* plan, uint32_t N, _Float16* xs, const PlanCheck& c,
                                  const int32_t* dst, uint32_t* bits, hipStream_t s) {
     if (c.snap_words > 1536u || c.snap_words2 > 1536u || c.status2 == nullptr) return hipErrorInvalidValue;
-    const uint32_t vpr = d / 8;
-    const uint32_t blocks = 1u + 8u * ((N + kGatherChunk - 1) / kGatherChunk);  // check + copy workgroups
-    gather_kernel<true><<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), rows, vpr, src, plan, N,
-                                               reinterpret_cast<u32x4*>(xs), c, dst, bits);
+    const uint32_t vpr = d / 8, parts = vpr / kGatherPart;
+    const uint32_t blocks = 1u + parts * ((N + kCountTile - 1) / kCountTile);  // check + copy workgroups
+    gather_kernel<true><<<blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(x), vpr, ids, hist, K, E, parts, plan,
+                                               N, reinterpret_cast<u32x4*>(xs), c, dst, bits);
     return hipGetLastError();
 }
 

@@ -355,8 +355,9 @@ void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupR
     });
     if (!fused) {
         add_step(seg, "gather", [=](hipStream_t st) {
-            return sm::launch_gather(reinterpret_cast<const _Float16*>(r.mixed), rows, d,
-                                     reinterpret_cast<const int32_t*>(r.src),
+            return sm::launch_gather(reinterpret_cast<const _Float16*>(r.mixed), d,
+                                     reinterpret_cast<const int32_t*>(r.ids),
+                                     reinterpret_cast<const uint32_t*>(r.hist), K, E,
                                      reinterpret_cast<const sm::Plan*>(r.plan), rows * K,
                                      reinterpret_cast<_Float16*>(r.gathered), st);
         });
@@ -364,8 +365,9 @@ void encode_grouping_launch(sm_segment* seg, const sm_moe_shape& s, const GroupR
     }
     const LayerChecks l = *lc;
     add_step(seg, "gather + expert checks", [=](hipStream_t st) {
-        return sm::launch_gather_checked(reinterpret_cast<const _Float16*>(r.mixed), rows, d,
-                                         reinterpret_cast<const int32_t*>(r.src),
+        return sm::launch_gather_checked(reinterpret_cast<const _Float16*>(r.mixed), d,
+                                         reinterpret_cast<const int32_t*>(r.ids),
+                                         reinterpret_cast<const uint32_t*>(r.hist), K, E,
                                          reinterpret_cast<const sm::Plan*>(r.plan), rows * K,
                                          reinterpret_cast<_Float16*>(r.gathered), l.check, l.dst, l.bits, st);
     });
