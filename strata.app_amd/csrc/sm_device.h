@@ -37,12 +37,12 @@ struct FromLds {
 
 // exp(x): Cody & Waite reduction x = n*ln2 + r with a two-part ln2, a degree-7 Taylor
 // polynomial in r evaluated by Horner with fma, and an exact scale by 2^n (v_ldexp_f32).
+// Branch-free: the polynomial runs on x clamped into [-104, 88.72...] (the identity inside it),
+// and the special cases are selected afterwards (NaN -> x, above -> +inf, below -> 0).
 __device__ __forceinline__ float exp_cw(float x) {
-    if (__builtin_isnan(x)) return x;
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (x < -104.0f) return 0.0f;
-    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 88.72283935546875f);
+    const float n = __builtin_rintf(xc * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
     r = __builtin_fmaf(-n, 1.428606765330187045e-06f, r);
     float p = 1.98412698412698412698e-4f;
     p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
@@ -52,7 +52,10 @@ __device__ __forceinline__ float exp_cw(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_amdgcn_ldexpf(p, int(n));
+    float e = __builtin_amdgcn_ldexpf(p, int(n));
+    e = x < -104.0f ? 0.0f : e;
+    e = x > 88.72283935546875f ? __builtin_inff() : e;
+    return __builtin_isnan(x) ? x : e;
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + exp_cw(-x)); }

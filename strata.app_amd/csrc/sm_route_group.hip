@@ -242,6 +242,42 @@ __device__ __forceinline__ void argmax_step(float& best, int32_t& who) {
     if (ob > best || (ob == best && ow < who)) { best = ob; who = ow; }
 }
 
+// Lane exchanges for one token's 32 lanes without the LDS crossbar: xor 16 swaps the two 16-lane
+// rows of the half-wave (v_permlane16_swap), xor 4 picks lane n ^ 4 from the two row rotations
+// by 4. Which output holds the partner is decided by applying the same exchange to the lane
+// numbers once per thread (XorSel), so the result does not rest on a reading of the operand
+// order. Used for the sums, whose xor order (16, 8, 4, 2, 1) fixes their bits.
+struct XorSel {
+    bool x16_first, x4_ror4;
+};
+__device__ __forceinline__ XorSel xor_sel(uint32_t lane) {
+    const auto r = __builtin_amdgcn_permlane16_swap(lane, lane, false, false);
+    const uint32_t ror4 = uint32_t(__builtin_amdgcn_mov_dpp(int(lane), 0x124, 0xF, 0xF, false));
+    return XorSel{r[0] == (lane ^ 16u), ror4 == (lane ^ 4u)};
+}
+__device__ __forceinline__ float xor16(float v, const XorSel& s) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, s.x16_first ? r[0] : r[1]);
+}
+__device__ __forceinline__ int32_t xor16(int32_t v, const XorSel& s) {
+    const auto r = __builtin_amdgcn_permlane16_swap(uint32_t(v), uint32_t(v), false, false);
+    return int32_t(s.x16_first ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor4(float v, const XorSel& s) {
+    const float a = dpp_f<0x124>(v), b = dpp_f<0x12C>(v);  // row_ror:4, row_ror:12
+    return s.x4_ror4 ? a : b;
+}
+// Butterfly sum over the token's 32 lanes in the reference's xor order.
+__device__ __forceinline__ float half_sum(float v, const XorSel& s) {
+    v = v + xor16(v, s);
+    v = v + dpp_f<0x128>(v);  // xor 8 (row_ror:8)
+    v = v + xor4(v, s);
+    v = v + dpp_f<0x4E>(v);   // xor 2
+    v = v + dpp_f<0xB1>(v);   // xor 1
+    return v;
+}
+
 template <int NV>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
                                                          int32_t* __restrict__ ids,
@@ -251,41 +287,47 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     const uint32_t L = threadIdx.x & 31u;
     const uint32_t t = (blockIdx.x * 256u + threadIdx.x) >> 5;
     const bool live = t < rows;
+    const XorSel xs = xor_sel(threadIdx.x & 63u);
+    // Every load is issued, clamped into the row (a dead token reads row 0), so the 32 lanes'
+    // loads go out together; padding slots are set to -inf afterwards.
     const float* row = logits + uint64_t(live ? t : 0u) * E;
     float v[NV];
-    float mx = kNegInf;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const uint32_t idx = L + 32u * i;
-        v[i] = (live && idx < E) ? row[idx] : kNegInf;
+        v[i] = row[idx < E ? idx : E - 1u];
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (L + 32u * i >= E) v[i] = kNegInf;
         mx = __builtin_fmaxf(mx, v[i]);
     }
     mx = __builtin_fmaxf(mx, dpp_f<0xB1>(mx));
     mx = __builtin_fmaxf(mx, dpp_f<0x4E>(mx));
     mx = __builtin_fmaxf(mx, dpp_f<0x124>(mx));
     mx = __builtin_fmaxf(mx, dpp_f<0x128>(mx));
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+    mx = __builtin_fmaxf(mx, xor16(mx, xs));
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        if (L + 32u * i < E) {
-            v[i] = exp_cw(v[i] - mx);
-            sum = sum + v[i];
-        }
+        const bool in = L + 32u * i < E;
+        const float e = exp_cw(v[i] - mx);
+        v[i] = in ? e : v[i];
+        sum = in ? sum + e : sum;
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off);
+    sum = half_sum(sum, xs);
     const float recip = 1.0f / sum;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        if (L + 32u * i < E) {
-            v[i] = v[i] * recip;
-            if (__builtin_isnan(v[i])) v[i] = -3.40282346638528859812e+38f;
-        } else {
-            v[i] = kNegInf;
-        }
+        float p = v[i] * recip;
+        if (__builtin_isnan(p)) p = -3.40282346638528859812e+38f;
+        v[i] = L + 32u * i < E ? p : kNegInf;
     }
+    // K rounds of argmax. Lane r keeps round r's id and value; the owner of each round's
+    // winner adds it to its share of the selected sum and retires that slot.
     float selected = 0.0f, sel_sum = 0.0f;
+    int32_t chosen = -1;
     for (uint32_t rank = 0; rank < K; ++rank) {
         // The lane's own argmax as a pairwise tree (depth log2 NV instead of a chain of NV - 1
         // dependent compares); the left, lower-index side wins ties, so the result is the
@@ -306,29 +348,30 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
         argmax_step<0x124>(best, who);
         argmax_step<0x128>(best, who);
         {
-            const float ob = __shfl_xor(best, 16);
-            const int32_t ow = __shfl_xor(who, 16);
+            const float ob = xor16(best, xs);
+            const int32_t ow = xor16(who, xs);
             if (ob > best || (ob == best && ow < who)) { best = ob; who = ow; }
         }
-        if ((uint32_t(who) & 31u) == L) {
-            const int slot = who >> 5;
+        const bool mine = (uint32_t(who) & 31u) == L;
+        const int slot = who >> 5;
 #pragma unroll
-            for (int i = 0; i < NV; ++i)
-                if (i == slot) v[i] = kNegInf;
-            if (live) {
-                const uint64_t entry = uint64_t(t) * K + rank;
-                ids[entry] = who;
-                if (hist != nullptr && uint32_t(who) < E) atomicAdd(&hist[(entry / kCountTile) * E + uint32_t(who)], 1u);
-            }
-            sel_sum = sel_sum + best;
+        for (int i = 0; i < NV; ++i)
+            if (mine && i == slot) v[i] = kNegInf;
+        sel_sum = mine ? sel_sum + best : sel_sum;
+        if (rank == L) {
+            selected = best;
+            chosen = who;
         }
-        if (rank == L) selected = best;
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) sel_sum = sel_sum + __shfl_xor(sel_sum, off);
+    sel_sum = half_sum(sel_sum, xs);
     const float ssum = __builtin_fmaxf(sel_sum, kWeightFloor);
     const float inv = 1.0f / ssum;
-    if (live && L < K) weights[uint64_t(t) * K + L] = divide ? selected / ssum : selected * inv;
+    if (live && L < K) {
+        const uint64_t entry = uint64_t(t) * K + L;
+        ids[entry] = chosen;
+        weights[entry] = divide ? selected / ssum : selected * inv;
+        if (hist != nullptr && uint32_t(chosen) < E) atomicAdd(&hist[(entry / kCountTile) * E + uint32_t(chosen)], 1u);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
