@@ -273,6 +273,126 @@ def measure_decode(moe, layer, ctx, name: str, steps: int, inputs=None):
     return out, inp
 
 
+def measure_tiered(moe, layer, gw, ctx, inp, steps: int):
+    """Configuration 2 with its odd experts in the cold tier: the layer's expert tensors are
+    written to a GGUF file (read back through the page cache), the routing segment marks the odd
+    experts' groups non-resident, the expert store resolves them into device slots
+    (sm_expert_store_resolve_layer: the plan read back, up to 8 reader threads, asynchronous
+    copies), and the expert segment runs on the slot addresses. Reported: the resolve time and
+    the whole layer call (routing segment, resolve, expert segment, synchronised) with every
+    cold expert read from the file (a fresh store each call) and with every one cached (one
+    store across calls), beside the same synchronised call at full residency."""
+    import ctypes as C
+    import tempfile
+
+    import numpy as np
+    import torch
+    cfg = layer.CONFIGS[2]
+    T, d, E, K, I = cfg.rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.expert_ff
+    sh = torch.cuda.current_stream().cuda_stream
+    out = {"workload": "config2:full_layer with the odd experts cold (GGUF file through the page cache)"}
+    with tempfile.TemporaryDirectory(prefix="strata_tiered_") as tdir:
+        path = Path(tdir) / "experts.gguf"
+        t0 = time.time()
+        gw.write_gguf(path, gw.expert_tensors([(inp.w_gate, inp.w_up, inp.w_down)], d, I, E,
+                                              moe.FORMAT_NAMES[cfg.gate_up_fmt], moe.FORMAT_NAMES[cfg.down_fmt]))
+        log(f"tiered: GGUF of {path.stat().st_size / 1e9:.2f} GB written in {time.time() - t0:.1f}s")
+        f = moe.GgufFile(path)
+        if not f:
+            raise RuntimeError(f.error)
+        L, err = f.expert_layout(1)
+        if L is None:
+            raise RuntimeError(err)
+        storage = ctx.register(torch.empty(L.total_bytes, dtype=torch.uint8, device="cuda"))
+        full = f.load_experts(ctx, sh, L, storage.view())
+        ws = layer.LayerWorkspace(ctx, cfg, inp, guard=False)
+        resident = np.zeros(E, np.int32)
+        resident[1::2] = -1
+        res_dev = ctx.register(torch.from_numpy(resident).cuda())
+        tiered = list(full)
+        for e in range(1, E, 2):
+            tiered[3 * e:3 * e + 3] = [0, 0, 0]
+        sb = moe.library().sm_expert_slot_bytes(C.byref(L))
+        per_half = E // 2
+        arena = ctx.register(torch.empty(2 * per_half * sb, dtype=torch.uint8, device="cuda"))
+
+        def call(store, cold: bool):
+            t_a = time.perf_counter()
+            rg = ws.route_gather_buffers()
+            if cold:
+                rg.resident = res_dev.view()
+            rg.layer = 0
+            seg = ctx.segment()
+            ok, err = seg.encode_prefill_moe_full_mode_route_gather(ws.shape, rg)
+            assert ok, err
+            ok, err = seg.encode_prefill_moe_shared_ffn(ws.shape, cfg.shared_fmt, ws.shared_buffers())
+            assert ok, err
+            seg.commit(sh)
+            leases, t_res, stats = None, 0.0, {}
+            addr = full
+            if cold:
+                leases = moe.LeaseSet(store)
+                table = (C.c_uint64 * len(tiered))(*tiered)
+                t_r = time.perf_counter()
+                ok, stats = store.resolve_layer(sh, 0, ws.plan.view(), leases, table)
+                t_res = time.perf_counter() - t_r
+                assert ok, stats
+                addr = list(table)
+            arena_v = arena.view() if cold else None
+            ws.gu_table = moe.ExpertTable(addr, ws.snap_gu.view(), [storage.view()], slot_arena=arena_v, leases=leases)
+            ws.dn_table = moe.ExpertTable(addr, ws.snap_dn.view(), [storage.view()], slot_arena=arena_v, leases=leases)
+            seg = ctx.segment()
+            for enc in (lambda s_: s_.encode_prefill_moe_gu(ws.shape, cfg.gate_up_fmt, ws.gate_up_buffers()),
+                        lambda s_: s_.encode_prefill_moe_down(ws.shape, cfg.down_fmt, ws.down_buffers()),
+                        lambda s_: s_.encode_prefill_moe_combine(ws.shape, ws.combine_buffers())):
+                ok, err = enc(seg)
+                assert ok, err
+            seg.commit(sh)
+            torch.cuda.synchronize()
+            if leases is not None:
+                leases.close()
+            return time.perf_counter() - t_a, t_res, stats
+
+        def store_new():
+            st = moe.ExpertStore(ctx, f, L, arena.view(), per_half)
+            if st.handle is None:
+                raise RuntimeError(st.error)
+            return st
+
+        for _ in range(3):
+            call(None, False)
+        full_ms = sorted(call(None, False)[0] for _ in range(max(5, steps)))[max(5, steps) // 2] * 1e3
+        miss, miss_res, miss_stats = [], [], {}
+        for _ in range(3):  # a fresh store each call: every cold expert read from the file
+            st = store_new()
+            w_, r_, miss_stats = call(st, True)
+            miss.append(w_)
+            miss_res.append(r_)
+            st.close()
+        st = store_new()
+        call(st, True)
+        hit, hit_res = [], []
+        for _ in range(max(5, steps)):  # one store: every cold expert cached in its slot
+            w_, r_, hit_stats = call(st, True)
+            hit.append(w_)
+            hit_res.append(r_)
+        st.close()
+        if ws.read_status(sh) != (0, 0, 0):
+            raise RuntimeError(f"tiered layer status {ws.read_status(sh)}")
+        med = lambda v: sorted(v)[len(v) // 2] * 1e3  # noqa: E731
+        out.update({
+            "cold_experts_used": int(miss_stats["lookups"]), "slot_bytes": int(sb),
+            "full_residency_sync_ms": round(full_ms, 3),
+            "all_miss": {"layer_ms": round(med(miss), 3), "resolve_ms": round(med(miss_res), 3),
+                         "file_bytes": int(miss_stats["file_bytes"]),
+                         "resolve_gbs": round(miss_stats["file_bytes"] / (med(miss_res) / 1e3) / 1e9, 2)},
+            "all_hit": {"layer_ms": round(med(hit), 3), "resolve_ms": round(med(hit_res), 3),
+                        "hits": int(hit_stats["hits"])},
+        })
+    log(f"tiered: {out}")
+    return out
+
+
 def cpu_description() -> dict:
     """The host the CPU baseline ran on: model name, logical CPUs, NUMA nodes."""
     model = "unknown"
@@ -305,6 +425,7 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-config3", action="store_true",
                     help="skip the configuration-3 (T=8192) grouped-GEMM figures")
+    ap.add_argument("--no-tiered", action="store_true", help="skip the tiered-residency figures")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-layer figures (T = 1 and 8 at the reference model's widths)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -416,6 +537,10 @@ def main() -> int:
         d1, _ = measure_decode(moe, layer, ctx, "window_t1", args.steps, inputs=dinp)
         extra["decode"] = {"t1": d1, "t8": d8}
         del dinp
+
+    # ---- tiered residency: configuration 2 with half of its experts in the cold tier ----
+    if args.config == 2 and not args.no_config3 and not args.no_tiered:
+        extra["tiered"] = measure_tiered(moe, layer, pkg.gguf_write, ctx, inp, args.steps)
 
     # ---- CPU baseline: the C++ restatement of the same stages on a bounded sample ----
     cpu = None
