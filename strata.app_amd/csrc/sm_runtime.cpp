@@ -37,6 +37,12 @@ struct sm_context {
     hipEvent_t ring_ev[kRingSlots] = {};
     bool ring_pending[kRingSlots] = {};
     bool ring_claimed[kRingSlots] = {};  // filled by an encode whose segment is not committed yet
+    // A step that reads two slots records one event, into its first slot's; the second slot
+    // (ring_alias = the first) is free once its partner is not pending. Every step that reads
+    // a ring slot runs on the commit's own stream, so a partner re-recorded later in the same
+    // commit completes after the earlier record, and one re-recorded by a later commit was
+    // claimed, and its earlier record waited on, first.
+    int ring_alias[kRingSlots] = {};
     uint32_t ring_next = 0;
     std::mutex ring_mu;
     // Second stream (default priority) for launches off the critical path of a full layer (the
@@ -451,7 +457,15 @@ int claim_ring_slot(sm_context* ctx, const std::vector<uint64_t>& table) {
         const uint32_t slot = ctx->ring_next++ % sm_context::kRingSlots;
         if (ctx->ring_claimed[slot]) continue;
         if (ctx->ring_pending[slot]) {
-            if (hipEventSynchronize(ctx->ring_ev[slot]) != hipSuccess) return -3;
+            int waited = slot;
+            if (ctx->ring_alias[slot] >= 0) {
+                const int a = ctx->ring_alias[slot];
+                waited = ctx->ring_pending[a] ? a : -1;
+            }
+            if (waited >= 0) {
+                if (hipEventSynchronize(ctx->ring_ev[waited]) != hipSuccess) return -3;
+                ctx->ring_pending[waited] = false;
+            }
             ctx->ring_pending[slot] = false;
         }
         ctx->ring_claimed[slot] = true;
@@ -853,8 +867,10 @@ sm_status sm_context_create(int device, sm_context** out) {
                   hipHostMalloc(reinterpret_cast<void**>(&c->ring),
                                 sizeof(uint64_t) * sm_context::kSlotWords * sm_context::kRingSlots,
                                 hipHostMallocDefault) == hipSuccess;
-        for (uint32_t i = 0; ok && i < sm_context::kRingSlots; ++i)
+        for (uint32_t i = 0; ok && i < sm_context::kRingSlots; ++i) {
+            c->ring_alias[i] = -1;
             ok = hipEventCreateWithFlags(&c->ring_ev[i], hipEventDisableTiming) == hipSuccess;
+        }
         ok = ok && hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) == hipSuccess &&
              hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming) == hipSuccess &&
              hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming) == hipSuccess;
@@ -873,7 +889,7 @@ void sm_context_destroy(sm_context* ctx) {
     // Teardown is best effort: a failed wait or release leaves nothing the caller can act on.
     for (uint32_t i = 0; i < sm_context::kRingSlots; ++i) {
         if (ctx->ring_ev[i] == nullptr) continue;
-        if (ctx->ring_pending[i]) (void)hipEventSynchronize(ctx->ring_ev[i]);
+        if (ctx->ring_pending[i] && ctx->ring_alias[i] < 0) (void)hipEventSynchronize(ctx->ring_ev[i]);
         (void)hipEventDestroy(ctx->ring_ev[i]);
     }
     if (ctx->ring) (void)hipHostFree(ctx->ring);
@@ -969,13 +985,20 @@ sm_status run_segment(sm_segment* seg, hipStream_t stream, hipEvent_t* ev) {
         if (st == SM_OK && ev && hipEventRecord(ev[2 * i], hs) != hipSuccess) st = SM_E_DEVICE;
         if (st == SM_OK && step.run(hs) != hipSuccess) st = SM_E_DEVICE;
         if (st == SM_OK && ev && hipEventRecord(ev[2 * i + 1], hs) != hipSuccess) st = SM_E_DEVICE;
-        for (const int slot : {step.ring_slot, step.ring_slot2}) {
-            if (slot < 0) continue;
+        const int s1 = step.ring_slot >= 0 ? step.ring_slot : step.ring_slot2;
+        const int s2 = step.ring_slot >= 0 ? step.ring_slot2 : -1;
+        if (s1 >= 0) {
             std::lock_guard<std::mutex> lk(ctx->ring_mu);
-            if (hipEventRecord(ctx->ring_ev[slot], hs) == hipSuccess)
-                ctx->ring_pending[slot] = true;
-            else
+            if (hipEventRecord(ctx->ring_ev[s1], hs) == hipSuccess) {
+                ctx->ring_pending[s1] = true;
+                ctx->ring_alias[s1] = -1;
+                if (s2 >= 0) {
+                    ctx->ring_pending[s2] = true;
+                    ctx->ring_alias[s2] = s1;
+                }
+            } else {
                 st = SM_E_DEVICE;
+            }
         }
     }
     if (side_open) join();
