@@ -267,7 +267,7 @@ def measure_decode(moe, layer, ctx, name: str, steps: int, inputs=None):
         "gate_up_matvec": fig(gu_w, us["decode gate/up"]),
         "down_matvec": fig(dn_w, us["decode down"]),
     }
-    if Is:
+    if Is and "decode shared gate/up" in us:  # below 4 rows they ride in the router's and the plan's launches
         out["shared_matvecs"] = fig(sh_w, us["decode shared gate/up"] + us["decode shared down"])
     log(f"decode {name}: {out}")
     return out, inp

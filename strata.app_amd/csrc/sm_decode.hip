@@ -153,7 +153,8 @@ struct DecodePlan {
 };
 static_assert(sizeof(DecodePlan) == 1620, "MoePlan layout");
 
-// First-appearance grouping of n = rows * top_k <= 80 entries, one 128-thread workgroup
+// First-appearance grouping of n = rows * top_k <= 80 entries, one workgroup of 128 or 256
+// threads (threads past 127 hold no entry)
 // (moe.metal:124-210): entry i's group is the rank of its expert's first appearance among
 // first appearances; its slot is the group's start plus the number of earlier entries with
 // the same expert. The groups' starts are a prefix sum of their sizes in first-appearance
@@ -172,7 +173,7 @@ __device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
         if (a.status != nullptr) *a.status = 0u;  // the stage's status word starts clear
     }
     const int32_t e = tid < n ? a.ids[tid] : -1;
-    e_s[tid] = e;
+    if (tid < 128u) e_s[tid] = e;  // a 256-thread workgroup (the fused front launch) runs it too
     __syncthreads();
     if (tid < n && (e < 0 || uint32_t(e) >= a.n_experts)) atomicOr(&bad_s, 1u);
     __syncthreads();
@@ -190,7 +191,7 @@ __device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
     const bool is_first = !bad && tid < n && first == tid;
     // Group index of a first appearance: first appearances before it (ballot prefix).
     const uint64_t m = __ballot(is_first);
-    if (lane == 0) {
+    if (lane == 0 && wave < 2u) {
         mask_s[wave][0] = uint32_t(m);
         mask_s[wave][1] = uint32_t(m >> 32);
     }
@@ -201,7 +202,7 @@ __device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
         const uint32_t y = __shfl_up(incl, off);
         if (lane >= off) incl += y;
     }
-    if (lane == 63u) size_w[wave] = incl;
+    if (lane == 63u && wave < 2u) size_w[wave] = incl;
     __syncthreads();
     const uint64_t m0 = uint64_t(mask_s[0][0]) | (uint64_t(mask_s[0][1]) << 32);
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64u - lane));
@@ -247,18 +248,6 @@ __device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
 }
 
 __global__ __launch_bounds__(128) void moe_plan_kernel(DecodePlanArgs a) { moe_plan_body(a); }
-
-// The plan (workgroup 0, 128 threads) and the Q8_1 quantization of the layer's F16 input rows
-// (the other workgroups, 128 values each) in one launch: neither reads what the other writes.
-__global__ __launch_bounds__(128) void plan_q8_1_kernel(DecodePlanArgs a, const _Float16* x, uint8_t* y, uint32_t n) {
-    if (blockIdx.x == 0) {
-        moe_plan_body(a);
-        return;
-    }
-    const uint32_t per_row = n / 128u, b = blockIdx.x - 1u;
-    const uint32_t r = b / per_row, i = (b - r * per_row) * 128u + threadIdx.x;
-    q8_1_value(f32_bits(float(x[uint64_t(r) * n + i])), y + uint64_t(r) * (n / 32u) * kQ81Bytes, i);
-}
 
 // ---- block dots over Q8_1 ----------------------------------------------------------------
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
@@ -411,7 +400,7 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
     // Every plan field this workgroup needs, read in one round trip (g < 80: all inside the plan).
     const uint32_t p_entries = P->n_entries, p_groups = P->n_groups;
     const int32_t p_s = P->grp_start[g], p_t = P->grp_start[g + 1], p_e = P->grp_e[g];
-    const bool plan_ok = p_entries == m.n_entries && p_groups <= 80u;
+    const bool plan_ok = p_entries == m.n_entries && p_groups <= m.n_entries;  // a group holds >= 1 entry
     if (!plan_ok) {
         if (g != 0u || blockIdx.x != 0u) return;
         if (tid == 0) atomicOr(m.status, 2u);
@@ -582,17 +571,19 @@ __device__ __forceinline__ void gate_logit_block(const DenseDecode& m) {
     }
 }
 
+// Workgroup bx of nb of one dense mat-vec (a launch of its own, or one part of a fused launch),
+// x_lds its dynamic LDS.
 template <int WT, bool GATE_UP, bool XF32, uint32_t LPR>
-__global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
-    if (GATE_UP && m.gv != nullptr && blockIdx.x == gridDim.x - 1u) {
-        gate_logit_block<WT>(m);  // the launch's last workgroup
+__device__ __forceinline__ void dense_decode_body(const DenseDecode& m, uint32_t bx, uint32_t nb, uint8_t* x_lds) {
+    if (GATE_UP && m.gv != nullptr && bx == nb - 1u) {
+        gate_logit_block<WT>(m);  // the job's last workgroup
         return;
     }
-    if (!GATE_UP && blockIdx.x >= m.row_blocks) {
+    if (!GATE_UP && bx >= m.row_blocks) {
         // The router launch's extra workgroups: one 8-byte word each per thread of the
         // validated address tables (pinned ring slots) into their device snapshots, read once
         // across PCIe beside the router's own work.
-        const uint32_t w = (blockIdx.x - m.row_blocks) * 256u + threadIdx.x;
+        const uint32_t w = (bx - m.row_blocks) * 256u + threadIdx.x;
         if (w < m.snap_words) m.snap_dst[w] = m.snap_src[w];
         else if (w - m.snap_words < m.snap_words2) m.snap_dst2[w - m.snap_words] = m.snap_src2[w - m.snap_words];
         return;
@@ -606,7 +597,6 @@ __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
     // (chunk, row). The copy is LDS-DMA, 1 KB per wave instruction (the allocation is rounded up
     // to whole kilobytes; lanes past the rows' end re-read their last 16 bytes into that tail),
     // issued before the first weight loads so that both are one round trip.
-    extern __shared__ __attribute__((aligned(1024))) uint8_t x_lds[];
     {
         const uint32_t xbytes = m.rows * m.k * (XF32 ? 4u : 2u);  // k % 64 == 0: whole 16-byte pieces
         const uint8_t* xg = reinterpret_cast<const uint8_t*>(m.x);
@@ -621,7 +611,7 @@ __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
     }
     const uint32_t nch = m.k / VPC;
     const uint32_t per_lane = (nch + LPR - 1u) / LPR;
-    const uint32_t row = matvec_rows_per_block(LPR) * blockIdx.x + wave * RPW + lane / LPR;
+    const uint32_t row = matvec_rows_per_block(LPR) * bx + wave * RPW + lane / LPR;
     const bool row_ok = row < m.n_out;  // uniform within each LPR-lane segment
     const uint32_t wbytes = WT == kWF32 ? 4u : 2u;
     float acc[NW][8];
@@ -727,16 +717,69 @@ __global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
     }
 }
 
+template <int WT, bool GATE_UP, bool XF32, uint32_t LPR>
+__global__ __launch_bounds__(256) void dense_decode_kernel(DenseDecode m) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t x_lds[];
+    dense_decode_body<WT, GATE_UP, XF32, LPR>(m, blockIdx.x, gridDim.x, x_lds);
+}
+
+// The decode layer's router (F32 rows, with its snapshot copies) and its shared expert's gate/up
+// (F16/BF16 rows, with the gate logit) in one launch: both read only the layer's F16 input
+// rows, staged alike, and neither reads what the other writes. Workgroups [0, r_blocks) are the
+// router's, the rest the shared gate/up's.
+template <int WT, uint32_t LPR>
+__global__ __launch_bounds__(256) void router_shared_decode_kernel(DenseDecode r, DenseDecode g, uint32_t r_blocks) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t x_lds[];
+    if (blockIdx.x < r_blocks) dense_decode_body<kWF32, false, false, LPR>(r, blockIdx.x, r_blocks, x_lds);
+    else dense_decode_body<WT, true, false, LPR>(g, blockIdx.x - r_blocks, gridDim.x - r_blocks, x_lds);
+}
+
+// A decode layer's front launch after the top-k: the plan (workgroup 0), the Q8_1 quantization
+// of its F16 input rows (the next q_blocks workgroups, 256 values each) and the shared expert's
+// down mat-vec (the remaining workgroups, F32 hidden rows; WT < 0: none). None of the three
+// reads what another writes.
+template <int WT, uint32_t LPR>
+__global__ __launch_bounds__(256) void decode_front_kernel(DecodePlanArgs a, const _Float16* x, uint8_t* y, uint32_t n,
+                                                           uint32_t q_blocks, DenseDecode sd) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t x_lds[];
+    if (blockIdx.x == 0) {
+        moe_plan_body(a);
+        return;
+    }
+    if (blockIdx.x <= q_blocks) {
+        const uint32_t per_row = (n + 255u) / 256u, b = blockIdx.x - 1u;
+        const uint32_t r = b / per_row, i = (b - r * per_row) * 256u + threadIdx.x;
+        if (i >= n) return;  // n % 32 == 0: whole 32-lane blocks leave together
+        q8_1_value(f32_bits(float(x[uint64_t(r) * n + i])), y + uint64_t(r) * (n / 32u) * kQ81Bytes, i);
+        return;
+    }
+    if constexpr (WT >= 0) {
+        const uint32_t first = 1u + q_blocks;
+        dense_decode_body<WT, false, true, LPR>(sd, blockIdx.x - first, gridDim.x - first, x_lds);
+    }
+}
+
+// Lanes per weight row: the smallest power of two from 8 to 64 that leaves each lane at most
+// kPerLane 16-byte chunks of a row of k values (VPC values per chunk).
+__host__ __device__ constexpr uint32_t dense_lpr(uint32_t k, uint32_t vpc) {
+    uint32_t lpr = 8;
+    while (lpr < 64u && (k / vpc + lpr - 1u) / lpr > kPerLane) lpr <<= 1;
+    return lpr;
+}
+
+// Workgroups of one dense job: its row blocks, then the gate-logit workgroup (gate/up with a
+// gate vector) or the snapshot-copy workgroups (router). Sets m.row_blocks.
+inline uint32_t dense_blocks(DenseDecode& m, bool gate_up, uint32_t lpr) {
+    m.row_blocks = (m.n_out + matvec_rows_per_block(lpr) - 1u) / matvec_rows_per_block(lpr);
+    const uint32_t extra = gate_up ? (m.gv != nullptr ? 1u : 0u) : (m.snap_words + m.snap_words2 + 255u) / 256u;
+    return m.row_blocks + extra;
+}
+
 template <int WT, bool GATE_UP, bool XF32>
 hipError_t launch_dense_decode_t(const DenseDecode& m, hipStream_t s) {
-    const uint32_t nch = m.k / (WT == kWF32 ? 4u : 8u);
-    uint32_t lpr = 8;
-    while (lpr < 64u && (nch + lpr - 1u) / lpr > kPerLane) lpr <<= 1;
+    const uint32_t lpr = dense_lpr(m.k, WT == kWF32 ? 4u : 8u);
     DenseDecode mm = m;
-    mm.row_blocks = (m.n_out + matvec_rows_per_block(lpr) - 1u) / matvec_rows_per_block(lpr);
-    // Extra workgroups: the gate logit (shared gate/up) or the snapshot copies (router).
-    const uint32_t extra = GATE_UP ? (m.gv != nullptr ? 1u : 0u) : (m.snap_words + m.snap_words2 + 255u) / 256u;
-    const dim3 grid(mm.row_blocks + extra);
+    const dim3 grid(dense_blocks(mm, GATE_UP, lpr));
     // The staged activation rows: rows x k values, at most 8 x SM_DECODE_MAX_WIDTH F32 (128 KB),
     // rounded up to whole kilobytes (the copy's unit).
     const size_t lds = (size_t(m.rows) * m.k * (XF32 ? 4u : 2u) + 1023u) & ~size_t(1023);
@@ -799,7 +842,7 @@ hipError_t launch_matvec_t(const DecodeMatvec& mm, hipStream_t s) {
     const uint32_t n_rows = MODE == kGateUp ? 2u * m.out_width : m.out_width;
     const uint32_t nblk = m.k / 32u, nunit = m.k / Unit::kVals;
     if (nunit == 0u || nunit > 64u || m.k % Unit::kVals != 0u) return hipErrorInvalidValue;  // host-checked
-    if (m.max_group == 0u || m.max_group > 8u) return hipErrorInvalidValue;
+    if (m.max_group == 0u || m.max_group > 8u || m.n_entries == 0u || m.n_entries > 80u) return hipErrorInvalidValue;
     uint32_t lpr = 1;
     while (lpr < nunit) lpr <<= 1;
     if (lpr < 8u) lpr = 8u;
@@ -810,7 +853,8 @@ hipError_t launch_matvec_t(const DecodeMatvec& mm, hipStream_t s) {
     const uint32_t slices = (n_rows + rpi - 1u) / rpi;
     const uint32_t per_iter = m.n_entries * slices;  // workgroups at one slice each (upper bound)
     m.iters = per_iter >= 4096u ? 4u : per_iter >= 2048u ? 2u : 1u;
-    const dim3 grid((slices + m.iters - 1u) / m.iters, 80);
+    // One grid row per possible group: a valid plan has at most one group per entry (<= 80).
+    const dim3 grid((slices + m.iters - 1u) / m.iters, m.n_entries);
     const size_t lds = size_t(m.max_group) * nblk * 9u * 4u + size_t(m.iters) * rpi * m.max_group * 4u;
     switch (lpr) {
         case 64: moe_matvec_kernel<Unit, MODE, 64><<<grid, 256, lds, s>>>(m); break;
@@ -830,11 +874,53 @@ hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_decode_plan_q8_1(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
-                                   hipStream_t s) {
-    if (n == 0u || n % 128u != 0u) return hipErrorInvalidValue;
-    plan_q8_1_kernel<<<1u + rows * (n / 128u), 128, 0, s>>>(a, x, y, n);
-    return hipGetLastError();
+namespace {
+template <int WT>
+hipError_t launch_front_t(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
+                          const DenseDecode* sd, hipStream_t s) {
+    const uint32_t q_blocks = rows * ((n + 255u) / 256u);
+    DenseDecode m = sd != nullptr ? *sd : DenseDecode{};
+    uint32_t lpr = 8, extra = 0;
+    size_t lds = 0;
+    if (WT >= 0) {
+        lpr = dense_lpr(m.k, 8u);
+        extra = dense_blocks(m, false, lpr);
+        lds = (size_t(m.rows) * m.k * 4u + 1023u) & ~size_t(1023);  // F32 hidden rows
+        if (lds > 131072u) return hipErrorInvalidValue;
+    }
+    const dim3 grid(1u + q_blocks + extra);
+    auto go = [&](auto kern) {
+        if (lds > 65536u) {
+            const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+            if (attr != hipSuccess) return attr;
+        }
+        kern<<<grid, 256, lds, s>>>(a, x, y, n, q_blocks, m);
+        return hipGetLastError();
+    };
+    if constexpr (WT < 0) {
+        return go(decode_front_kernel<-1, 8>);
+    } else {
+        switch (lpr) {
+            case 64: return go(decode_front_kernel<WT, 64>);
+            case 32: return go(decode_front_kernel<WT, 32>);
+            case 16: return go(decode_front_kernel<WT, 16>);
+            default: return go(decode_front_kernel<WT, 8>);
+        }
+    }
+}
+}  // namespace
+
+hipError_t launch_decode_front(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
+                               Fmt shared_fmt, const DenseDecode* shared_down, hipStream_t s) {
+    if (rows == 0u || rows > 8u || n == 0u || n % 32u != 0u) return hipErrorInvalidValue;
+    if (shared_down == nullptr) return launch_front_t<-1>(a, x, y, n, rows, nullptr, s);
+    if (shared_down->rows != rows || shared_down->k == 0u || shared_down->k % 64u != 0u) return hipErrorInvalidValue;
+    switch (shared_fmt) {
+        case Fmt::F16: return launch_front_t<kWF16>(a, x, y, n, rows, shared_down, s);
+        case Fmt::BF16: return launch_front_t<kWBF16>(a, x, y, n, rows, shared_down, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_swiglu_q8_1(const float* gate, const float* up, float* hidden, uint8_t* y, uint32_t n, uint32_t rows,
@@ -876,9 +962,9 @@ hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipS
     }
 }
 
-hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
-                                uint32_t d, uint32_t E, const SnapshotCopy& snap, hipStream_t s) {
-    if (rows == 0u || rows > 8u || d == 0u || d % 64u != 0u) return hipErrorInvalidValue;
+namespace {
+DenseDecode router_job(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows, uint32_t d,
+                       uint32_t E, const SnapshotCopy& snap) {
     DenseDecode m{};
     m.snap_src = snap.src;
     m.snap_dst = snap.dst;
@@ -893,7 +979,52 @@ hipError_t launch_router_decode(const _Float16* x, const float* w, const float* 
     m.rows = rows;
     m.k = d;
     m.n_out = E;
-    return launch_dense_decode_t<kWF32, false, false>(m, s);
+    return m;
+}
+
+template <int WT>
+hipError_t launch_router_shared_t(DenseDecode r, DenseDecode g, uint32_t lpr, hipStream_t s) {
+    const uint32_t rb = dense_blocks(r, false, lpr), gb = dense_blocks(g, true, lpr);
+    const size_t lds = (size_t(r.rows) * r.k * 2u + 1023u) & ~size_t(1023);  // F16 rows, as one job stages them
+    if (lds > 131072u) return hipErrorInvalidValue;
+    auto go = [&](auto kern) {
+        if (lds > 65536u) {
+            const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+            if (attr != hipSuccess) return attr;
+        }
+        kern<<<rb + gb, 256, lds, s>>>(r, g, rb);
+        return hipGetLastError();
+    };
+    switch (lpr) {
+        case 64: return go(router_shared_decode_kernel<WT, 64>);
+        case 32: return go(router_shared_decode_kernel<WT, 32>);
+        case 16: return go(router_shared_decode_kernel<WT, 16>);
+        default: return go(router_shared_decode_kernel<WT, 8>);
+    }
+}
+}  // namespace
+
+hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
+                                uint32_t d, uint32_t E, const SnapshotCopy& snap, hipStream_t s) {
+    if (rows == 0u || rows > 8u || d == 0u || d % 64u != 0u) return hipErrorInvalidValue;
+    return launch_dense_decode_t<kWF32, false, false>(router_job(x, w, bias, logits, rows, d, E, snap), s);
+}
+
+hipError_t launch_router_shared_decode(const _Float16* x, const float* w, const float* bias, float* logits,
+                                       uint32_t rows, uint32_t d, uint32_t E, const SnapshotCopy& snap, Fmt shared_fmt,
+                                       const DenseDecode& shared_gate_up, hipStream_t s) {
+    if (rows == 0u || rows > 8u || d == 0u || d % 64u != 0u) return hipErrorInvalidValue;
+    if (shared_gate_up.rows != rows || shared_gate_up.k != d || shared_gate_up.x != x) return hipErrorInvalidValue;
+    if (shared_fmt != Fmt::F16 && shared_fmt != Fmt::BF16) return hipErrorInvalidValue;
+    const DenseDecode r = router_job(x, w, bias, logits, rows, d, E, snap);
+    const uint32_t lpr = dense_lpr(d, 4u);
+    if (lpr != dense_lpr(d, 8u)) {  // the two jobs split their rows differently: two launches
+        const hipError_t e = launch_dense_decode_t<kWF32, false, false>(r, s);
+        return e != hipSuccess ? e : launch_dense_decode(shared_fmt, true, shared_gate_up, s);
+    }
+    return shared_fmt == Fmt::F16 ? launch_router_shared_t<kWF16>(r, shared_gate_up, lpr, s)
+                                  : launch_router_shared_t<kWBF16>(r, shared_gate_up, lpr, s);
 }
 
 hipError_t launch_swiglu_f32(const float* gate, const float* up, float* out, uint64_t n, hipStream_t s) {

@@ -190,9 +190,6 @@ struct DecodePlanArgs {
     uint32_t rows, top_k, n_experts;
 };
 hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t s);
-// The plan and the Q8_1 quantization of rows x n F16 input values (n a multiple of 128), one launch.
-hipError_t launch_decode_plan_q8_1(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
-                                   hipStream_t s);
 // hidden = silu(gate) * up (F32, rows x n, n a multiple of 32) and its Q8_1 blocks y, one launch.
 hipError_t launch_swiglu_q8_1(const float* gate, const float* up, float* hidden, uint8_t* y, uint32_t n, uint32_t rows,
                               hipStream_t s);
@@ -253,6 +250,15 @@ hipError_t launch_dense_decode(Fmt fmt, bool gate_up, const DenseDecode& m, hipS
 // The launch also copies the validated address tables of `snap` into their device snapshots.
 hipError_t launch_router_decode(const _Float16* x, const float* w, const float* bias, float* logits, uint32_t rows,
                                 uint32_t d, uint32_t E, const SnapshotCopy& snap, hipStream_t s);
+// The router above and the shared expert's gate/up (launch_dense_decode with gate_up, x the same
+// F16 rows) in one launch.
+hipError_t launch_router_shared_decode(const _Float16* x, const float* w, const float* bias, float* logits,
+                                       uint32_t rows, uint32_t d, uint32_t E, const SnapshotCopy& snap, Fmt shared_fmt,
+                                       const DenseDecode& shared_gate_up, hipStream_t s);
+// The plan, the Q8_1 quantization of rows x n F16 input values (n a multiple of 32) and, when
+// shared_down is given, the shared expert's down mat-vec (launch_dense_decode, down) in one launch.
+hipError_t launch_decode_front(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
+                               Fmt shared_fmt, const DenseDecode* shared_down, hipStream_t s);
 // out = (p_0 w_0 + sum_r fma) + shared * sigmoid(gl); shared == null: no shared term.
 hipError_t launch_combine_decode(const float* parts, const float* w, const float* shared, const float* gl, float* out,
                                  uint32_t rows, uint32_t top_k, uint32_t d, hipStream_t s);

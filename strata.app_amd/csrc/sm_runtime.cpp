@@ -1743,10 +1743,9 @@ bool check_shared_decode(Check& c, const sm_moe_shape& s, int fmt, const sm_shar
            c.view(b.gate_logit, uint64_t(s.rows) * 4, 4, "shared gate logit", true, r.gl);
 }
 
-// side: both launches go to the context's second stream (a decode layer's shared expert runs
-// beside its routed chain).
-void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r,
-                                 bool side = false) {
+// The decode shared expert's two mat-vecs: gate/up (with the gate logit), then down.
+struct SharedDecodeJobs { sm::DenseDecode gu, dn; };
+SharedDecodeJobs shared_decode_jobs(const sm_moe_shape& s, const SharedRes& r) {
     sm::DenseDecode gu{};
     gu.w0 = reinterpret_cast<const uint8_t*>(r.wg);
     gu.w1 = reinterpret_cast<const uint8_t*>(r.wu);
@@ -1764,6 +1763,15 @@ void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt
     dn.rows = s.rows;
     dn.k = s.shared_ff;
     dn.n_out = s.hidden;
+    return {gu, dn};
+}
+
+// side: both launches go to the context's second stream (a decode layer's shared expert runs
+// beside its routed chain).
+void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r,
+                                 bool side = false) {
+    const SharedDecodeJobs j = shared_decode_jobs(s, r);
+    const sm::DenseDecode gu = j.gu, dn = j.dn;
     add_step(seg, "decode shared gate/up", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), true, gu, st); },
              side);
     add_step(seg, "decode shared down", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), false, dn, st); },
@@ -2008,30 +2016,39 @@ sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape,
     snap.src2 = s_dn >= 0 ? seg->ctx->ring + uint64_t(s_dn) * sm_context::kSlotWords : nullptr;
     snap.dst2 = reinterpret_cast<uint64_t*>(fr.dn.w.snapshot);
     snap.words2 = s_dn >= 0 ? uint32_t(fr.dn.w.table.size()) : 0u;
+    // The shared expert reads only the layer's input and its own weights, and only the combine
+    // reads its outputs (the alias checks above). From 4 rows up it runs on the context's
+    // second stream from the layer's start, beside the routed chain (T = 8 at the reference
+    // model's widths: 120.7 -> 111.7 us per layer). Below that the fork and join cost more than
+    // the overlap gains (T = 1: 55.5 -> 62-67 us), so its two mat-vecs ride in launches of the
+    // routed chain instead: gate/up in the router's, down in the plan's.
+    const bool side = s.shared_ff != 0 && s.rows >= 4;
+    const bool fused = s.shared_ff != 0 && !side;
+    const SharedDecodeJobs sj = s.shared_ff != 0 ? shared_decode_jobs(s, sr) : SharedDecodeJobs{};
+    const Fmt sfmt = Fmt(f->shared);
     const size_t first = seg->steps.size();
-    add_step(seg, "decode router", [=](hipStream_t st2) {
-        return sm::launch_router_decode(reinterpret_cast<const _Float16*>(rr.x), reinterpret_cast<const float*>(rr.w),
-                                        reinterpret_cast<const float*>(rr.bias), reinterpret_cast<float*>(rr.logits), rows,
-                                        d, E, snap, st2);
+    add_step(seg, fused ? "decode router + shared gate/up" : "decode router", [=](hipStream_t st2) {
+        const auto* x = reinterpret_cast<const _Float16*>(rr.x);
+        const auto* w = reinterpret_cast<const float*>(rr.w);
+        const auto* bias = reinterpret_cast<const float*>(rr.bias);
+        auto* logits = reinterpret_cast<float*>(rr.logits);
+        if (fused) return sm::launch_router_shared_decode(x, w, bias, logits, rows, d, E, snap, sfmt, sj.gu, st2);
+        return sm::launch_router_decode(x, w, bias, logits, rows, d, E, snap, st2);
     });
     seg->steps.back().ring_slot = s_gu;
     seg->steps.back().ring_slot2 = s_dn;
     encode_route_launch(seg, s, 0, ro);  // multiply mode (the Window's route)
     const sm::DecodePlanArgs pa = decode_plan_args(s, pr);
     const uintptr_t x = rr.x;
-    add_step(seg, "decode plan + Q8_1 input", [=](hipStream_t st2) {
-        return sm::launch_decode_plan_q8_1(pa, reinterpret_cast<const _Float16*>(x), reinterpret_cast<uint8_t*>(xq), d,
-                                           rows, st2);
+    add_step(seg, fused ? "decode plan + Q8_1 input + shared down" : "decode plan + Q8_1 input", [=](hipStream_t st2) {
+        return sm::launch_decode_front(pa, reinterpret_cast<const _Float16*>(x), reinterpret_cast<uint8_t*>(xq), d, rows,
+                                       sfmt, fused ? &sj.dn : nullptr, st2);
     });
     if ((st = encode_routed_ffn_launch(seg, s, f->gate_up, f->down, fr, true)) != SM_OK) return st;
-    // The shared expert reads only the layer's input and its own weights, and only the combine
-    // reads its outputs (the alias checks above), so from 4 rows up it runs on the context's
-    // second stream from the layer's start, beside the routed chain (T = 8 at the reference
-    // model's widths: 120.7 -> 111.7 us per layer). At T = 1 the fork and join cost more than
-    // the overlap gains (55.5 -> 62-67 us), so one row stays on the caller's stream.
-    const bool side = s.shared_ff != 0 && s.rows >= 4;
-    if (side) seg->steps[first].fork_before = true;
-    if (s.shared_ff != 0) encode_shared_decode_launch(seg, s, f->shared, sr, side);
+    if (side) {
+        seg->steps[first].fork_before = true;
+        encode_shared_decode_launch(seg, s, f->shared, sr, true);
+    }
     encode_combine_decode_launch(seg, s, cr, side);
     return SM_OK;
 }

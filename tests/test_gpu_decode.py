@@ -225,6 +225,14 @@ def test_null_expert_and_damaged_plan(moe, layer, orc, gpu_ctx, stream):
     gu.run(gpu_ctx, stream, lambda s: s.encode_moe_experts(cfg.shape(), cfg.gate_up_fmt, eb, keep=tg))
     assert gu.host(b_st, np.uint32)[0] == 2
     assert (gu.host(b_g, np.float32) == 0).all() and (gu.host(b_u, np.float32) == 0).all()
+    # more groups than entries (each group holds at least one): the same
+    bad = plan.copy()
+    bad[0:4] = np.frombuffer(np.uint32(N + 1).tobytes(), np.uint8)
+    b_plan.tensor.copy_(gu.dev(bad))
+    b_g.tensor.fill_(0x7F)
+    gu.run(gpu_ctx, stream, lambda s: s.encode_moe_experts(cfg.shape(), cfg.gate_up_fmt, eb, keep=tg))
+    assert gu.host(b_st, np.uint32)[0] == 2
+    assert (gu.host(b_g, np.float32) == 0).all() and (gu.host(b_u, np.float32) == 0).all()
 
 
 # ---- post-ops and the shared expert ----------------------------------------------------------
