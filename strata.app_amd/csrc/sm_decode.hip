@@ -13,6 +13,7 @@
 
 #include "sm_device.h"
 #include "sm_launch.h"
+#include "sm_topk.h"
 
 namespace sm {
 namespace {
@@ -159,7 +160,8 @@ static_assert(sizeof(DecodePlan) == 1620, "MoePlan layout");
 // first appearances; its slot is the group's start plus the number of earlier entries with
 // the same expert. The groups' starts are a prefix sum of their sizes in first-appearance
 // order. An id outside [0, E) sets status bit 1 and leaves an empty plan (n_groups = 0).
-__device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
+// ids_lds (may be null): the route ids, already in LDS.
+__device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a, const int32_t* ids_lds = nullptr) {
     __shared__ int32_t e_s[128];
     __shared__ uint32_t mask_s[2][2];
     __shared__ uint32_t size_w[2];
@@ -172,7 +174,7 @@ __device__ __forceinline__ void moe_plan_body(const DecodePlanArgs& a) {
         bad_s = 0;
         if (a.status != nullptr) *a.status = 0u;  // the stage's status word starts clear
     }
-    const int32_t e = tid < n ? a.ids[tid] : -1;
+    const int32_t e = tid < n ? (ids_lds != nullptr ? ids_lds[tid] : a.ids[tid]) : -1;
     if (tid < 128u) e_s[tid] = e;  // a 256-thread workgroup (the fused front launch) runs it too
     __syncthreads();
     if (tid < n && (e < 0 || uint32_t(e) >= a.n_experts)) atomicOr(&bad_s, 1u);
@@ -734,16 +736,31 @@ __global__ __launch_bounds__(256) void router_shared_decode_kernel(DenseDecode r
     else dense_decode_body<WT, true, false, LPR>(g, blockIdx.x - r_blocks, gridDim.x - r_blocks, x_lds);
 }
 
-// A decode layer's front launch after the top-k: the plan (workgroup 0), the Q8_1 quantization
-// of its F16 input rows (the next q_blocks workgroups, 256 values each) and the shared expert's
-// down mat-vec (the remaining workgroups, F32 hidden rows; WT < 0: none). None of the three
-// reads what another writes.
+// A decode layer's front launch after the router: the plan (workgroup 0; with a.logits, the
+// top-k first, its ids handed to the plan through LDS), the Q8_1 quantization of the F16 input
+// rows (the next q_blocks workgroups, 256 values each) and the shared expert's down mat-vec
+// (the remaining workgroups, F32 hidden rows; WT < 0: none). None of the three reads what
+// another writes.
 template <int WT, uint32_t LPR>
 __global__ __launch_bounds__(256) void decode_front_kernel(DecodePlanArgs a, const _Float16* x, uint8_t* y, uint32_t n,
                                                            uint32_t q_blocks, DenseDecode sd) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t x_lds[];
     if (blockIdx.x == 0) {
-        moe_plan_body(a);
+        if (a.logits == nullptr) {
+            moe_plan_body(a);
+            return;
+        }
+        // The route first: up to 4 tokens one per wave, up to 8 two per wave (slots for E <= 512).
+        __shared__ int32_t ids_s[80];
+        const uint32_t wave = threadIdx.x >> 6;
+        if (a.rows <= 4u)
+            topk_token<8, true>(a.logits, a.route_ids, a.route_weights, a.rows, a.n_experts, a.top_k, 0, nullptr, wave,
+                                ids_s);
+        else
+            topk_token<16, false>(a.logits, a.route_ids, a.route_weights, a.rows, a.n_experts, a.top_k, 0, nullptr,
+                                  threadIdx.x >> 5, ids_s);
+        __syncthreads();
+        moe_plan_body(a, ids_s);
         return;
     }
     if (blockIdx.x <= q_blocks) {
@@ -913,7 +930,10 @@ hipError_t launch_front_t(const DecodePlanArgs& a, const _Float16* x, uint8_t* y
 
 hipError_t launch_decode_front(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
                                Fmt shared_fmt, const DenseDecode* shared_down, hipStream_t s) {
-    if (rows == 0u || rows > 8u || n == 0u || n % 32u != 0u) return hipErrorInvalidValue;
+    if (rows == 0u || rows > 8u || n == 0u || n % 32u != 0u || a.rows != rows) return hipErrorInvalidValue;
+    if (a.logits != nullptr && (a.n_experts == 0u || a.n_experts > 512u || a.top_k == 0u || a.top_k > a.n_experts ||
+                                rows * a.top_k > 80u || a.route_ids == nullptr || a.route_weights == nullptr))
+        return hipErrorInvalidValue;
     if (shared_down == nullptr) return launch_front_t<-1>(a, x, y, n, rows, nullptr, s);
     if (shared_down->rows != rows || shared_down->k == 0u || shared_down->k % 64u != 0u) return hipErrorInvalidValue;
     switch (shared_fmt) {

@@ -188,6 +188,12 @@ struct DecodePlanArgs {
     uint8_t* plan;              // the layer's MoePlan
     uint32_t* status;           // bit 1 on an id outside [0, E) (may be null)
     uint32_t rows, top_k, n_experts;
+    // launch_decode_front only (may be null): the route's logits [rows][E]; the launch's plan
+    // workgroup then runs the top-k (multiply mode) first, into route_ids (the buffer `ids`
+    // names) and route_weights.
+    const float* logits;
+    int32_t* route_ids;
+    float* route_weights;
 };
 hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t s);
 // hidden = silu(gate) * up (F32, rows x n, n a multiple of 32) and its Q8_1 blocks y, one launch.
@@ -255,8 +261,9 @@ hipError_t launch_router_decode(const _Float16* x, const float* w, const float* 
 hipError_t launch_router_shared_decode(const _Float16* x, const float* w, const float* bias, float* logits,
                                        uint32_t rows, uint32_t d, uint32_t E, const SnapshotCopy& snap, Fmt shared_fmt,
                                        const DenseDecode& shared_gate_up, hipStream_t s);
-// The plan, the Q8_1 quantization of rows x n F16 input values (n a multiple of 32) and, when
-// shared_down is given, the shared expert's down mat-vec (launch_dense_decode, down) in one launch.
+// The plan (after the top-k when a.logits is given), the Q8_1 quantization of rows x n F16 input
+// values (n a multiple of 32) and, when shared_down is given, the shared expert's down mat-vec
+// (launch_dense_decode, down) in one launch. E <= 512.
 hipError_t launch_decode_front(const DecodePlanArgs& a, const _Float16* x, uint8_t* y, uint32_t n, uint32_t rows,
                                Fmt shared_fmt, const DenseDecode* shared_down, hipStream_t s);
 // out = (p_0 w_0 + sum_r fma) + shared * sigmoid(gl); shared == null: no shared term.

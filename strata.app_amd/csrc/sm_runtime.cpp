@@ -1713,14 +1713,13 @@ void encode_swiglu_f32_launch(sm_segment* seg, uintptr_t g, uintptr_t u, uintptr
     });
 }
 
-// join: the combine waits for the shared expert's launches on the context's second stream.
-void encode_combine_decode_launch(sm_segment* seg, const sm_moe_shape& s, const CombineRes& r, bool join = false) {
+void encode_combine_decode_launch(sm_segment* seg, const sm_moe_shape& s, const CombineRes& r) {
     const auto rows = s.rows, K = s.top_k, d = s.hidden;
     add_step(seg, "decode combine", [=](hipStream_t st) {
         return sm::launch_combine_decode(reinterpret_cast<const float*>(r.parts), reinterpret_cast<const float*>(r.weights),
                                          reinterpret_cast<const float*>(r.shared), reinterpret_cast<const float*>(r.gate),
                                          reinterpret_cast<float*>(r.out), rows, K, d, st);
-    }, false, join);
+    });
 }
 
 // The decode shared expert over F16/BF16 weights: the hidden view holds F32 [T][Is] (the
@@ -1766,16 +1765,11 @@ SharedDecodeJobs shared_decode_jobs(const sm_moe_shape& s, const SharedRes& r) {
     return {gu, dn};
 }
 
-// side: both launches go to the context's second stream (a decode layer's shared expert runs
-// beside its routed chain).
-void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r,
-                                 bool side = false) {
+void encode_shared_decode_launch(sm_segment* seg, const sm_moe_shape& s, int fmt, const SharedRes& r) {
     const SharedDecodeJobs j = shared_decode_jobs(s, r);
     const sm::DenseDecode gu = j.gu, dn = j.dn;
-    add_step(seg, "decode shared gate/up", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), true, gu, st); },
-             side);
-    add_step(seg, "decode shared down", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), false, dn, st); },
-             side);
+    add_step(seg, "decode shared gate/up", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), true, gu, st); });
+    add_step(seg, "decode shared down", [=](hipStream_t st) { return sm::launch_dense_decode(Fmt(fmt), false, dn, st); });
 }
 
 // The routed FFN's scratch and output views (gate, up, hidden, Q8_1 hidden, parts, status).
@@ -2017,16 +2011,13 @@ sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape,
     snap.dst2 = reinterpret_cast<uint64_t*>(fr.dn.w.snapshot);
     snap.words2 = s_dn >= 0 ? uint32_t(fr.dn.w.table.size()) : 0u;
     // The shared expert reads only the layer's input and its own weights, and only the combine
-    // reads its outputs (the alias checks above). From 4 rows up it runs on the context's
-    // second stream from the layer's start, beside the routed chain (T = 8 at the reference
-    // model's widths: 120.7 -> 111.7 us per layer). Below that the fork and join cost more than
-    // the overlap gains (T = 1: 55.5 -> 62-67 us), so its two mat-vecs ride in launches of the
-    // routed chain instead: gate/up in the router's, down in the plan's.
-    const bool side = s.shared_ff != 0 && s.rows >= 4;
-    const bool fused = s.shared_ff != 0 && !side;
-    const SharedDecodeJobs sj = s.shared_ff != 0 ? shared_decode_jobs(s, sr) : SharedDecodeJobs{};
+    // reads its outputs (the alias checks above), so its two mat-vecs ride in launches of the
+    // routed chain: gate/up in the router's, down in the plan's. At the reference model's widths
+    // this beats running them on a second stream beside the chain, whose fork and join cost more
+    // than the overlap gains (T = 1: 48.0 -> 41.1 us per layer, T = 8: 104.4 -> 97.6 us).
+    const bool fused = s.shared_ff != 0;
+    const SharedDecodeJobs sj = fused ? shared_decode_jobs(s, sr) : SharedDecodeJobs{};
     const Fmt sfmt = Fmt(f->shared);
-    const size_t first = seg->steps.size();
     add_step(seg, fused ? "decode router + shared gate/up" : "decode router", [=](hipStream_t st2) {
         const auto* x = reinterpret_cast<const _Float16*>(rr.x);
         const auto* w = reinterpret_cast<const float*>(rr.w);
@@ -2037,19 +2028,19 @@ sm_status sm_encode_moe_decode_layer(sm_segment* seg, const sm_moe_shape* shape,
     });
     seg->steps.back().ring_slot = s_gu;
     seg->steps.back().ring_slot2 = s_dn;
-    encode_route_launch(seg, s, 0, ro);  // multiply mode (the Window's route)
-    const sm::DecodePlanArgs pa = decode_plan_args(s, pr);
+    // The route (multiply mode, the Window's) runs in the plan's workgroup of the next launch.
+    sm::DecodePlanArgs pa = decode_plan_args(s, pr);
+    pa.logits = reinterpret_cast<const float*>(ro.logits);
+    pa.route_ids = reinterpret_cast<int32_t*>(ro.ids);
+    pa.route_weights = reinterpret_cast<float*>(ro.weights);
     const uintptr_t x = rr.x;
-    add_step(seg, fused ? "decode plan + Q8_1 input + shared down" : "decode plan + Q8_1 input", [=](hipStream_t st2) {
+    add_step(seg, fused ? "decode top-k + plan + Q8_1 input + shared down" : "decode top-k + plan + Q8_1 input",
+             [=](hipStream_t st2) {
         return sm::launch_decode_front(pa, reinterpret_cast<const _Float16*>(x), reinterpret_cast<uint8_t*>(xq), d, rows,
                                        sfmt, fused ? &sj.dn : nullptr, st2);
     });
     if ((st = encode_routed_ffn_launch(seg, s, f->gate_up, f->down, fr, true)) != SM_OK) return st;
-    if (side) {
-        seg->steps[first].fork_before = true;
-        encode_shared_decode_launch(seg, s, f->shared, sr, true);
-    }
-    encode_combine_decode_launch(seg, s, cr, side);
+    encode_combine_decode_launch(seg, s, cr);
     return SM_OK;
 }
 

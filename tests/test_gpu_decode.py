@@ -329,10 +329,20 @@ def layer_ref(orc, cfg, inp, ws_ids, ws_logits):
     return orc.combine_decode(parts.astype(np.float32), w, sh, gl, T, K, d), plan, xq
 
 
-@pytest.mark.parametrize("name", ["window_t1", "window_t8", "full_layer_t8", "low_bit_t4"])
+def _extra_decode(layer, moe, name):
+    """Small layers for the two top-k layouts of the front launch (one token per wave up to 4
+    rows, two per wave above) at expert counts that leave most slots as padding, one without
+    a shared expert."""
+    return {"small_t3": layer.LayerConfig("small_t3", 3, 512, 40, 5, 256, 256, moe.Q4_K, moe.Q8_0, moe.F16,
+                                          seed=0x5EED0D02),
+            "small_t6": layer.LayerConfig("small_t6", 6, 512, 100, 7, 256, 0, moe.Q8_0, moe.Q8_0, moe.F16,
+                                          seed=0x5EED0D03)}[name]
+
+
+@pytest.mark.parametrize("name", ["window_t1", "window_t8", "full_layer_t8", "low_bit_t4", "small_t3", "small_t6"])
 def test_decode_layer(moe, layer, orc, gpu_ctx, stream, name):
     print(f"case decode layer {name}", flush=True)
-    cfg = layer.DECODE_CONFIGS[name]
+    cfg = layer.DECODE_CONFIGS[name] if name in layer.DECODE_CONFIGS else _extra_decode(layer, moe, name)
     inp = _inputs(layer, cfg)
     ws = layer.DecodeWorkspace(gpu_ctx, cfg, inp)
     ws.out.tensor.fill_(float("nan"))
