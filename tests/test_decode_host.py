@@ -114,13 +114,13 @@ def test_decode_coordinators_encode(moe, fd):
     sfb.shared.hidden = fd.sh_h.view(0, fd.shape.rows * fd.shape.shared_ff * 2)  # an F16-sized hidden
     ok, err, _ = fd.run(lambda s: s.encode_moe_shared_ffn(fd.shape, moe.F16, sfb))
     assert not ok and "shared hidden view is undersized" in err
-    # router, top-k, plan + Q8_1, gate/up, SwiGLU + Q8_1, down, shared x2, combine
+    # router + shared gate/up, top-k + plan + Q8_1 input + shared down, gate/up, SwiGLU + Q8_1, down, combine
     ok, err, n = fd.run(lambda s: s.encode_moe_decode_layer(fd.shape, fd.fmts, fd.layer_buffers()))
     assert ok, err
-    assert n == 9
-    ns = shape_with(moe, fd.shape, shared_ff=0)
+    assert n == 6
+    ns = shape_with(moe, fd.shape, shared_ff=0)  # the same launches without the shared expert's parts
     ok, err, n = fd.run(lambda s: s.encode_moe_decode_layer(ns, fd.fmts, fd.layer_buffers()))
-    assert ok and n == 7, err
+    assert ok and n == 6, err
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -186,6 +186,6 @@ def test_decode_reference_model_widths(moe):
     of that width are rejected."""
     fd = FakeDecode(moe, T=8, d=2560, E=64, K=10, I=640, Is=640, fmt_gu=2, fmt_dn=1)
     ok, err, n = fd.run(lambda s: s.encode_moe_decode_layer(fd.shape, fd.fmts, fd.layer_buffers()))
-    assert ok and n == 9, err
+    assert ok and n == 6, err
     ok, err, _ = fd.run(lambda s: s.encode_moe_routed_ffn(fd.shape, moe.Q4_K, moe.Q4_K, fd.routed()))
     assert not ok and "expert weight extent is invalid" in err
