@@ -471,18 +471,51 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
     uint32_t* codes_s = act_s;                                               // [entry][block][8]
     float* d_s = reinterpret_cast<float*>(act_s + m.max_group * nblk * 8u);  // [entry][block]
     float* res_s = d_s + m.max_group * nblk;                                 // [slice row][entry]
-    // Stage the group's activation blocks: n_e rows of nblk Q8_1 blocks.
-    for (uint32_t i = tid; i < n_e * nblk * 9u; i += 256u) {
+    // Stage the group's activation blocks (n_e rows of nblk Q8_1 blocks) into LDS. The first
+    // kStageRegs words per thread are loaded into registers before the first slice's weight
+    // units are requested and stored after, so the two round trips overlap (the loads return in
+    // order, so storing the staged words waits only for them); the barrier then waits for the
+    // LDS stores alone and leaves the weight loads in flight.
+    constexpr uint32_t kStageRegs = 4;
+    const uint32_t n_words = n_e * nblk * 9u;  // >= 9
+    const uint32_t d_base = m.max_group * nblk * 8u;
+    auto stage_src = [&](uint32_t i) {
         const uint32_t c = i / (nblk * 9u), rem = i - c * nblk * 9u, b = rem / 9u, w = rem - b * 9u;
-        const uint32_t v = ld_global<uint32_t>(m.act + (uint64_t(arow[c]) * nblk + b) * kQ81Bytes + 4u * w);
-        if (w == 0u) d_s[c * nblk + b] = f16_lo(v);
-        else codes_s[(c * nblk + b) * 8u + (w - 1u)] = v;
+        return m.act + (uint64_t(arow[c]) * nblk + b) * kQ81Bytes + 4u * w;
+    };
+    // LDS word of staged word i: its block's d (as F32) or one of its 8 code words.
+    auto stage_dst = [&](uint32_t i, uint32_t& v) {
+        const uint32_t c = i / (nblk * 9u), rem = i - c * nblk * 9u, b = rem / 9u, w = rem - b * 9u;
+        v = w == 0u ? f32_bits(f16_lo(v)) : v;
+        return w == 0u ? d_base + c * nblk + b : (c * nblk + b) * 8u + (w - 1u);
+    };
+    // Branch-free, so the stores wait for the staged words only: loads clamped into the range,
+    // and a thread past it stores to the first result word, which the first slice overwrites.
+    uint32_t sv[kStageRegs];
+#pragma unroll
+    for (uint32_t j = 0; j < kStageRegs; ++j) {
+        const uint32_t i = tid + 256u * j;
+        sv[j] = ld_global<uint32_t>(stage_src(i < n_words ? i : n_words - 1u));
     }
-    __syncthreads();
+    uint32_t r[Unit::kRaw];
+    Unit::raw(row_ptr(0u), u, r);
+#pragma unroll
+    for (uint32_t j = 0; j < kStageRegs; ++j) {
+        const uint32_t i = tid + 256u * j;
+        uint32_t v = sv[j];
+        const uint32_t at = stage_dst(i < n_words ? i : n_words - 1u, v);
+        act_s[i < n_words ? at : d_base + m.max_group * nblk] = v;
+    }
+    if (n_words > 256u * kStageRegs)  // more than eight entries' worth at d = 2560: the rest in the plain way
+        for (uint32_t i = tid + 256u * kStageRegs; i < n_words; i += 256u) {
+            uint32_t v = ld_global<uint32_t>(stage_src(i));
+            const uint32_t at = stage_dst(i, v);  // converts v first
+            act_s[at] = v;
+        }
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     for (uint32_t it = 0; it < m.iters; ++it) {
         const uint32_t lr = it * RPI + wave * RPW + (lane_ok ? rin : 0u);
-        uint32_t r[Unit::kRaw];
-        Unit::raw(row_ptr(it), u, r);
+        if (it > 0u) Unit::raw(row_ptr(it), u, r);
         // One entry at a time (n_e is uniform over the workgroup): the unit's sub-blocks against
         // the entry's activation blocks, then the butterfly over the row's LPR lanes.
         for (uint32_t c = 0; c < n_e; ++c) {
