@@ -375,7 +375,9 @@ typedef struct sm_moe_shared_ffn_buffers {
 
 /* One decode layer: router GEMM, top-k in multiply mode (the Window's route, moe_dispatch.hpp:
  * 161-168), plan (+ both address snapshots), Q8_1 of the input, the routed FFN, the shared
- * expert (F16/BF16 mat-vecs on mixed_h, as sm_encode_moe_shared_ffn) and the decode combine. */
+ * expert (F16/BF16 mat-vecs on mixed_h, as sm_encode_moe_shared_ffn) and the decode combine, as
+ * six launches on the commit's stream: router with the shared gate/up; top-k, plan, Q8_1 input
+ * and shared down; routed gate/up; SwiGLU + Q8_1; routed down; combine. */
 typedef struct sm_decode_layer_buffers {
     sm_view mixed_h;            /* F16 [T,d]                                                */
     sm_view router_weights;     /* F32 [E,d]                                                */
