@@ -336,10 +336,15 @@ def _extra_decode(layer, moe, name):
     return {"small_t3": layer.LayerConfig("small_t3", 3, 512, 40, 5, 256, 256, moe.Q4_K, moe.Q8_0, moe.F16,
                                           seed=0x5EED0D02),
             "small_t6": layer.LayerConfig("small_t6", 6, 512, 100, 7, 256, 0, moe.Q8_0, moe.Q8_0, moe.F16,
-                                          seed=0x5EED0D03)}[name]
+                                          seed=0x5EED0D03),
+            "small_t2": layer.LayerConfig("small_t2", 2, 512, 64, 8, 256, 256, moe.Q4_K, moe.Q8_0, moe.F16,
+                                          seed=0x5EED0D04),
+            "small_t1": layer.LayerConfig("small_t1", 1, 512, 40, 5, 256, 0, moe.Q4_K, moe.Q8_0, moe.F16,
+                                          seed=0x5EED0D05)}[name]
 
 
-@pytest.mark.parametrize("name", ["window_t1", "window_t8", "full_layer_t8", "low_bit_t4", "small_t3", "small_t6"])
+@pytest.mark.parametrize("name", ["window_t1", "window_t8", "full_layer_t8", "low_bit_t4", "small_t3", "small_t6",
+                                  "small_t2", "small_t1"])
 def test_decode_layer(moe, layer, orc, gpu_ctx, stream, name):
     print(f"case decode layer {name}", flush=True)
     cfg = layer.DECODE_CONFIGS[name] if name in layer.DECODE_CONFIGS else _extra_decode(layer, moe, name)
@@ -368,6 +373,12 @@ def test_decode_layer(moe, layer, orc, gpu_ctx, stream, name):
     want, plan, xq = layer_ref(orc, cfg, inp, ids, logits)
     assert np.array_equal(gu.host(ws.plans, np.uint8), plan)
     assert np.array_equal(gu.host(ws.xq, np.uint8).reshape(T, -1), xq)
+    # The SwiGLU rows and their Q8_1 blocks follow from the GPU's own gate/up rows bit for bit.
+    N, I = T * K, cfg.expert_ff
+    g_rows, u_rows = gu.host(ws.gate, np.float32).reshape(N, I), gu.host(ws.up, np.float32).reshape(N, I)
+    hid = gu.host(ws.hidden, np.float32).reshape(N, I)
+    assert np.array_equal(hid.view(np.uint32), orc.swiglu_f32(g_rows, u_rows).view(np.uint32)), "decode SwiGLU rows"
+    assert np.array_equal(gu.host(ws.hq, np.uint8).reshape(N, -1), orc.quantize_q8_1(hid)), "decode Q8_1 hidden"
     out = gu.host(ws.out, np.float32).reshape(T, d)
     assert np.isfinite(out).all()
     err, rel = gu.layer_tolerance(out, want)
@@ -378,3 +389,40 @@ def test_decode_layer(moe, layer, orc, gpu_ctx, stream, name):
     ws.run(stream)
     torch.cuda.synchronize()
     assert np.array_equal(gu.host(ws.out, np.float32).reshape(T, d).view(np.uint32), first.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["window_t1", "window_t8"])
+def test_decode_layer_null_expert_address(moe, layer, orc, gpu_ctx, stream, name):
+    """A routed expert without an up matrix: status bit 0, its group's gate/up rows, SwiGLU rows
+    and parts zero, the other groups unchanged."""
+    print(f"case decode layer null expert {name}", flush=True)
+    import torch
+    cfg = layer.DECODE_CONFIGS[name]
+    inp = _inputs(layer, cfg)
+    ws = layer.DecodeWorkspace(gpu_ctx, cfg, inp)
+    ws.run(stream)
+    torch.cuda.synchronize()
+    assert ws.read_status() == 0
+    T, d, K, I = cfg.rows, cfg.hidden, cfg.top_k, cfg.expert_ff
+    N = T * K
+    good_gate = gu.host(ws.gate, np.float32).reshape(N, I).copy()
+    good_out = gu.host(ws.out, np.float32).reshape(T, d).copy()
+    victim = int(gu.host(ws.ids, np.int32)[0])
+    addr = list(ws.addresses)
+    addr[3 * victim + 1] = 0
+    ws.gu_table = moe.ExpertTable(addr, ws.snap_gu.view(), [ws.w_gate.view(), ws.w_up.view()])
+    ws.run(stream)
+    torch.cuda.synchronize()
+    assert ws.read_status() == 1
+    pf = _plan_fields(orc, gu.host(ws.plans, np.uint8))
+    gi = list(pf["grp_e"][: int(pf["n_groups"])]).index(victim)
+    a0, a1 = int(pf["grp_start"][gi]), int(pf["grp_start"][gi + 1])
+    gate = gu.host(ws.gate, np.float32).reshape(N, I)
+    assert (gate[a0:a1] == 0).all() and (gu.host(ws.hidden, np.float32).reshape(N, I)[a0:a1] == 0).all()
+    keep = np.r_[0:a0, a1:N]
+    assert np.array_equal(gate[keep].view(np.uint32), good_gate[keep].view(np.uint32))
+    parts = gu.host(ws.parts, np.float32).reshape(N, d)
+    dst = pf["ent_dst"][a0:a1]
+    assert (parts[dst] == 0).all()
+    out = gu.host(ws.out, np.float32).reshape(T, d)
+    assert np.isfinite(out).all() and not np.array_equal(out, good_out)
