@@ -90,8 +90,8 @@ struct ProdQ4K {
     __device__ __forceinline__ void prepare() { q4k_pair_scales(hdr, g, d_lo, m_lo, d_hi, m_hi); }
     __device__ __forceinline__ half8 chunk(int s) const {
         const int w = 2 * (s & 1);
-        if (s < 2) return decode8(qs[w] & 0x0F0F0F0Fu, qs[w + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
-        return decode8(qs[w] & 0xF0F0F0F0u, qs[w + 1] & 0xF0F0F0F0u, d_hi, m_hi);
+        if (s < 2) return decode8_nib(qs[w] & 0x0F0F0F0Fu, qs[w + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
+        return decode8_nib((qs[w] >> 4) & 0x0F0F0F0Fu, (qs[w + 1] >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
     }
 };
 
@@ -156,12 +156,11 @@ struct ProdQ2K {
         const uint32_t jj = uint32_t(s >> 1);
         const uint32_t shift = 2u * (2u * (g & 1u) + jj);
         const uint32_t scb = (sc >> (8u * (2u * jj + b))) & 0xffu;
-        const float dl = d * float(scb & 0xFu);
-        const float ml = -(dmin * float(scb >> 4));
+        const Q2Table t = q2_table(d * float(scb & 0xFu), -(dmin * float(scb >> 4)));
         const int w = 2 * (s & 1);
         const uint32_t x0 = (qs[w] >> shift) & 0x03030303u;
         const uint32_t x1 = (qs[w + 1] >> shift) & 0x03030303u;
-        return decode8(x0, x1, dl, ml);
+        return lookup8(x0, x1, t);
     }
 };
 
