@@ -132,9 +132,10 @@ __device__ __forceinline__ half8 decode8(uint32_t w0, uint32_t w1, float scale, 
 
 // 2-bit codes by table: a 16-value group of one scale byte takes only the four values
 // fma(dl, q, ml), q = 0..3, each rounded to F32 and then F16 as decode8 rounds it. The
-// table holds their low bytes in `lo` and high bytes in `hi` (byte q of each), so a value of
-// code q is bytes q and 4 + q of the pair {hi:lo}: one v_perm_b32 builds the byte indices
-// of two values and a second selects them.
+// table holds their low bytes in `lo` and high bytes in `hi` (byte q of each). A dword of four
+// codes (one per byte, each <= 3) is itself a v_perm_b32 selector into either half, so two
+// permutes give the four values' low and high bytes and two more interleave them into F16
+// pairs.
 struct Q2Table {
     uint32_t lo, hi;
 };
@@ -147,11 +148,11 @@ __device__ __forceinline__ Q2Table q2_table(float dl, float ml) {
 __device__ __forceinline__ half8 lookup8(uint32_t x0, uint32_t x1, const Q2Table& t) {
     half2v p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t x = i < 2 ? x0 : x1;
-        // {q_a, 4 + q_a, q_b, 4 + q_b} for the value pair (a, b) = (0, 1) or (2, 3)
-        const uint32_t idx = __builtin_amdgcn_perm(x | 0x04040404u, x, (i & 1) ? 0x07030602u : 0x05010400u);
-        p[i] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(t.hi, t.lo, idx));
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t x = i == 0 ? x0 : x1;
+        const uint32_t lo = __builtin_amdgcn_perm(0u, t.lo, x), hi = __builtin_amdgcn_perm(0u, t.hi, x);
+        p[2 * i] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, 0x05010400u));
+        p[2 * i + 1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, 0x07030602u));
     }
     return half8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
 }
