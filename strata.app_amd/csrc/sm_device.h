@@ -105,33 +105,30 @@ __device__ __forceinline__ half2v cvt_pk_f16(float a, float b) {
     return __builtin_convertvector(float2v{a, b}, half2v);
 }
 
-// Keeps a masked dword opaque to the backend so it does not narrow the mask into per-value
-// bit-field extracts; each byte then converts with one v_cvt_f32_ubyte{0..3}.
-__device__ __forceinline__ uint32_t keep_u32(uint32_t v) {
-    __asm__("" : "+v"(v));
-    return v;
+// A code byte b <= 15 read as an OCP E4M3 value is exactly b * 2^-9 (b < 8: the subnormal
+// b/8 * 2^-6; 8 <= b <= 15: (1 + (b - 8)/8) * 2^-6), so one v_cvt_pk_f32_fp8 turns two code
+// bytes into exact F32 values, where v_cvt_f32_ubyte{j} takes one instruction per byte.
+__device__ __forceinline__ float2v nib_pair(uint32_t w, bool hi_word) {
+    return hi_word ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true) : __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
 }
 
-// Eight values fma(scale, byte_j, bias) from the four bytes of two dwords, rounded to F32
-// and then to F16 in pairs (v_fma_f32, then v_cvt_pk_f16_f32: two separate roundings). With
-// every byte < 2^8 and scale carrying <= 17 significant bits the product is exact, so this
-// equals the reference's `scale * q - bias` in F32, then F16.
-__device__ __forceinline__ half8 decode8(uint32_t w0, uint32_t w1, float scale, float bias) {
-    w0 = keep_u32(w0);
-    w1 = keep_u32(w1);
-    float f[8];
+// Eight values fma(scale, q_j, bias) from the code bytes q_j <= 15 of two dwords, rounded to
+// F32 and then to F16 in pairs (v_fma_f32, then v_cvt_pk_f16_f32: two separate roundings),
+// given scale512 = 512 * scale (exact: a power-of-two factor on a normal F32). The product
+// 512 scale * (q 2^-9) is scale * q exactly, and with scale carrying <= 17 significant bits
+// and q < 2^4 it is exact in F32, so this equals the reference's `scale * q - bias` in F32,
+// then F16.
+__device__ __forceinline__ half8 decode8_nib(uint32_t w0, uint32_t w1, float scale512, float bias) {
+    const float2v q[4] = {nib_pair(w0, false), nib_pair(w0, true), nib_pair(w1, false), nib_pair(w1, true)};
+    half2v p[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        f[j] = __builtin_fmaf(scale, ubyte(w0, j), bias);
-        f[4 + j] = __builtin_fmaf(scale, ubyte(w1, j), bias);
-    }
-    const half2v p0 = cvt_pk_f16(f[0], f[1]), p1 = cvt_pk_f16(f[2], f[3]);
-    const half2v p2 = cvt_pk_f16(f[4], f[5]), p3 = cvt_pk_f16(f[6], f[7]);
-    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    for (int i = 0; i < 4; ++i)
+        p[i] = cvt_pk_f16(__builtin_fmaf(scale512, q[i][0], bias), __builtin_fmaf(scale512, q[i][1], bias));
+    return half8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
 }
 
 // 2-bit codes by table: a 16-value group of one scale byte takes only the four values
-// fma(dl, q, ml), q = 0..3, each rounded to F32 and then F16 as decode8 rounds it. The
+// fma(dl, q, ml), q = 0..3, each rounded to F32 and then F16 as decode8_nib rounds it. The
 // table holds their low bytes in `lo` and high bytes in `hi` (byte q of each). A dword of four
 // codes (one per byte, each <= 3) is itself a v_perm_b32 selector into either half, so two
 // permutes give the four values' low and high bytes and two more interleave them into F16
@@ -172,10 +169,8 @@ __device__ __forceinline__ half8 lookup8(uint32_t x0, uint32_t x1, const Q2Table
 // X = {b[2g], b[2g+1], b[2g+4], b[2g+5]} (g < 2) or {b[2g+4], b[2g+5]} twice (g >= 2) and
 // Y = {b[2g-4], b[2g-3], b[2g], b[2g+1]}; then V = (X & m1) | ((X >> 4) & m3) | ((Y >> 2) & m2)
 // with (m1, m3, m2) = (0x3F3F3F3F, 0, 0) for g < 2 and (0x0F0F, 0x0F0F0000, 0x30303030) for
-// g >= 2, since (y >> 2) & 0x30 == (y >> 6) << 4 for a byte y. The high-nibble scale is
-// divided by 16 (exact in F32: d * scale >= 2^-24): those values are converted in place as
-// 16 * q (q & 0xF0), so fma(d_hi / 16, 16 q, m_hi) is the same single rounding of
-// d_hi * q + m_hi.
+// g >= 2, since (y >> 2) & 0x30 == (y >> 6) << 4 for a byte y. The scales are returned
+// premultiplied by 512 for decode8_nib (exact: d * scale is 0 or at least 2^-24).
 __device__ __forceinline__ void q4k_pair_scales(const u32x4& hdr, uint32_t g, float& d_lo, float& m_lo, float& d_hi,
                                                 float& m_hi) {
     const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
@@ -186,8 +181,8 @@ __device__ __forceinline__ void q4k_pair_scales(const u32x4& hdr, uint32_t g, fl
     const uint32_t y = __builtin_amdgcn_perm(hdr[2], hdr[1], sel_lo);
     const uint32_t v = (x & (hi_pairs ? 0x00000F0Fu : 0x3F3F3F3Fu)) | ((x >> 4) & (hi_pairs ? 0x0F0F0000u : 0u)) |
                        ((y >> 2) & (hi_pairs ? 0x30303030u : 0u));
-    d_lo = d * ubyte(v, 0);
-    d_hi = d * ubyte(v, 1) * 0.0625f;
+    d_lo = d * ubyte(v, 0) * 512.0f;
+    d_hi = d * ubyte(v, 1) * 512.0f;
     m_lo = -(dmin * ubyte(v, 2));
     m_hi = -(dmin * ubyte(v, 3));
 }
@@ -209,8 +204,8 @@ struct FragQ4K {
     __device__ __forceinline__ void prepare() { q4k_pair_scales(hdr, uint32_t(g), d_lo, m_lo, d_hi, m_hi); }
     __device__ __forceinline__ uint32_t q(int i) const { return i < 4 ? qa[i] : qb[i - 4]; }
     __device__ __forceinline__ half8 step(int s) const {
-        if (s < 4) return decode8(q(2 * s) & 0x0F0F0F0Fu, q(2 * s + 1) & 0x0F0F0F0Fu, d_lo, m_lo);
-        return decode8(q(2 * s - 8) & 0xF0F0F0F0u, q(2 * s - 7) & 0xF0F0F0F0u, d_hi, m_hi);
+        if (s < 4) return decode8_nib(q(2 * s) & 0x0F0F0F0Fu, q(2 * s + 1) & 0x0F0F0F0Fu, d_lo, m_lo);
+        return decode8_nib((q(2 * s - 8) >> 4) & 0x0F0F0F0Fu, (q(2 * s - 7) >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
     }
 };
 

@@ -90,8 +90,8 @@ struct ProdQ4K {
     __device__ __forceinline__ void prepare() { q4k_pair_scales(hdr, g, d_lo, m_lo, d_hi, m_hi); }
     __device__ __forceinline__ half8 chunk(int s) const {
         const int w = 2 * (s & 1);
-        if (s < 2) return decode8(qs[w] & 0x0F0F0F0Fu, qs[w + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
-        return decode8(qs[w] & 0xF0F0F0F0u, qs[w + 1] & 0xF0F0F0F0u, d_hi, m_hi);
+        if (s < 2) return decode8_nib(qs[w] & 0x0F0F0F0Fu, qs[w + 1] & 0x0F0F0F0Fu, d_lo, m_lo);
+        return decode8_nib((qs[w] >> 4) & 0x0F0F0F0Fu, (qs[w + 1] >> 4) & 0x0F0F0F0Fu, d_hi, m_hi);
     }
 };
 
