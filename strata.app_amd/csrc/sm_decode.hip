@@ -452,7 +452,8 @@ __global__ __launch_bounds__(256, 4) void moe_matvec_kernel(DecodeMatvec m) {  /
             const bool up = MODE == kGateUp && i >= m.out_width;
             float* out = up ? m.out1 : m.out0;
             const uint32_t col = up ? i - m.out_width : i;
-            for (uint32_t c = 0; c < n_e; ++c) out[uint64_t(orow[c]) * m.out_width + col] = 0.0f;
+            for (uint32_t c = 0; c < n_e; ++c)  // a damaged entry's row cannot be named: skipped
+                if (orow[c] < m.n_entries) out[uint64_t(orow[c]) * m.out_width + col] = 0.0f;
         }
         if (tid == 0 && blockIdx.x == 0u) atomicOr(m.status, fault);
         return;

@@ -7,7 +7,7 @@ the same Q8_1 codes and weight blocks, within 32 F32 roundings of the block term
 (a lane sums at most a few blocks, then a butterfly of at most six steps). The layer output is
 checked against a composed oracle within the layer bound (max-abs 2e-2, rel-L2 5e-3 in F16).
 Failure paths are forced from the host (a null expert address, out-of-range ids, a damaged
-plan header): every kernel still exits normally.
+plan header, route destinations that name no row): every kernel still exits normally.
 """
 import numpy as np
 import pytest
@@ -233,6 +233,56 @@ def test_null_expert_and_damaged_plan(moe, layer, orc, gpu_ctx, stream):
     gu.run(gpu_ctx, stream, lambda s: s.encode_moe_experts(cfg.shape(), cfg.gate_up_fmt, eb, keep=tg))
     assert gu.host(b_st, np.uint32)[0] == 2
     assert (gu.host(b_g, np.float32) == 0).all() and (gu.host(b_u, np.float32) == 0).all()
+
+
+def test_down_damaged_destinations(moe, layer, orc, gpu_ctx, stream):
+    """A plan whose route destinations (ent_dst) name no row: the down stage reports status bit 1,
+    zeroes the named rows of the groups holding such an entry, and writes nothing for the entry
+    that names none (its real destination row keeps its old bytes); every other group's rows are
+    the FP64 products."""
+    print("case decode down with damaged destinations", flush=True)
+    T, K, E, d, I = 8, 10, 40, 1024, 512
+    cfg = layer.LayerConfig("dec_dst", T, d, E, K, I, 0, moe.Q4_K, moe.Q8_0, moe.F16, seed=0x5EED0D0D)
+    inp = layer.make_inputs(cfg)
+    rng = np.random.default_rng(77)
+    ids = _ids(rng, T, K, E)
+    plan, _ = orc.moe_plan(ids, E)
+    xq = orc.quantize_q8_1(inp.x[:T].view(np.float16).astype(np.float32))
+    N = T * K
+    hq = orc.quantize_q8_1((rng.standard_normal((N, I)) * 0.05).astype(np.float32))
+    _, _, _, _, parts, pm = routed_ref(orc, cfg, inp, plan, xq, hq)
+    pf = _plan_fields(orc, plan)
+    bad = plan.copy()
+    bf = bad.view(orc.PLAN_DTYPE)[0]
+    g1, g2 = 1, 2
+    e1, e2 = int(pf["grp_start"][g1]), int(pf["grp_start"][g2])  # first entry of each group
+    lost = [int(pf["ent_dst"][e1]), int(pf["ent_dst"][e2])]
+    bf["ent_dst"][e1] = -1
+    bf["ent_dst"][e2] = N + 7
+    bw_d = gpu_ctx.register(gu.dev(inp.w_down))
+    addr = []
+    for e in range(E):
+        addr += [0, 0, bw_d.ptr + e * inp.dn_stride]
+    snap = gpu_ctx.register(gu.poison(E * 24))
+    td = moe.ExpertTable(addr, snap.view(), [bw_d.view()])
+    b_hq, b_plan = gpu_ctx.register(gu.dev(hq)), gpu_ctx.register(gu.dev(bad))
+    b_p, b_st = gpu_ctx.register(gu.poison(N * d * 4)), gpu_ctx.register(gu.dev(np.zeros(1, np.uint32)))
+    db = moe.MoeDownBuffers(td.struct, b_hq.view(), b_plan.view(), b_p.view(), b_st.view())
+    gu.run(gpu_ctx, stream, lambda s: s.encode_moe_down(cfg.shape(), moe.Q8_0, db, keep=td))
+    assert gu.host(b_st, np.uint32)[0] == 2
+    got = gu.host(b_p, np.uint32).reshape(N, d)
+    poison = np.full(d, 0xA5A5A5A5, np.uint32)  # gu.poison's fill byte
+    damaged = set()
+    for g in (g1, g2):
+        for a in range(int(pf["grp_start"][g]), int(pf["grp_start"][g + 1])):
+            dst = int(bf["ent_dst"][a])
+            if 0 <= dst < N:
+                damaged.add(dst)
+                assert (got[dst] == 0).all(), f"row {dst} of a damaged group not zeroed"
+    for row in lost:
+        assert np.array_equal(got[row], poison), f"row {row} written although no entry names it"
+    keep = np.array([r for r in range(N) if r not in damaged and r not in lost])
+    _within(got.view(np.float32)[keep], parts[keep], pm[keep], "down parts beside the damaged groups")
 
 
 # ---- post-ops and the shared expert ----------------------------------------------------------
