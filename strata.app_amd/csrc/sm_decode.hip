@@ -862,21 +862,34 @@ __global__ __launch_bounds__(256) void swiglu_f32_kernel(const float* gate, cons
 }
 
 // The decode combine (moe.metal:253-274): the first rank is a product, the others fma in
-// rank order, and the gated shared output is added last.
+// rank order, and the gated shared output is added last. The ranks' values are loaded eight at
+// a time (a rank past top_k reloads the last one and is not used) before their fmas, so a
+// thread keeps eight loads in flight instead of paying one round trip per rank.
+constexpr uint32_t kCombineBatch = 8;
 __global__ __launch_bounds__(256) void combine_decode_kernel(const float* parts, const float* w, const float* shared,
                                                              const float* gl, float* out, uint32_t top_k, uint32_t d) {
     const uint32_t t = blockIdx.y, c = blockIdx.x * 256u + threadIdx.x;
     if (c >= d) return;
     const float* p = parts + uint64_t(t) * top_k * d + c;
     const float* wt = w + uint64_t(t) * top_k;
-    float s = p[0] * wt[0];
-    for (uint32_t k = 1; k < top_k; ++k) s = __builtin_fmaf(p[uint64_t(k) * d], wt[k], s);
-    float o = s;
-    if (shared != nullptr) {
-        const float gs = sigmoid(gl[t]);
-        o = s + shared[uint64_t(t) * d + c] * gs;
+    // The shared row's value and gate logit go out with the first batch.
+    const float sh = shared != nullptr ? shared[uint64_t(t) * d + c] : 0.0f;
+    const float g = shared != nullptr ? gl[t] : 0.0f;
+    float s = 0.0f;
+    for (uint32_t k0 = 0; k0 < top_k; k0 += kCombineBatch) {
+        float pv[kCombineBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kCombineBatch; ++j) {
+            const uint32_t k = k0 + j < top_k ? k0 + j : top_k - 1u;
+            pv[j] = p[uint64_t(k) * d];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kCombineBatch; ++j) {
+            const uint32_t k = k0 + j;
+            if (k < top_k) s = k == 0u ? pv[j] * wt[0] : __builtin_fmaf(pv[j], wt[k], s);
+        }
     }
-    out[uint64_t(t) * d + c] = o;
+    out[uint64_t(t) * d + c] = shared != nullptr ? s + sh * sigmoid(g) : s;
 }
 
 // Copies a validated address table (pinned host ring slot) into its device snapshot and clears
