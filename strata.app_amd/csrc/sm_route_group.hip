@@ -593,24 +593,37 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
     const uint64_t entry = uint64_t(i0) + tid;
     const int32_t id = entry < N ? ids[entry] : -1;  // issued before the plan reads
     for (uint32_t e = tid; e < E; e += 256u) s_base[e] = hist[uint64_t(tile) * E + e];
+    // CHECK: this workgroup's share of the tile's destinations, loaded with the other first
+    // loads and marked after the copies (a returning atomic would hold the copies behind its
+    // round trip).
+    bool marks = false;
+    uint32_t dv = 0;
     if constexpr (CHECK) {
         const uint32_t per = (kCountTile + parts - 1u) / parts;
         const uint32_t i = i0 + part * per + tid;
-        if (tid < per && i < i1) {
-            const uint32_t dv = uint32_t(dst[i]);
-            if (dv >= N) {
-                atomicOr(c.status2, 2u);
-            } else {
-                const uint32_t mask = 1u << (dv % 32u);
-                if (atomicOr(&bits[dv / 32u], mask) & mask) atomicOr(c.status2, 2u);
-            }
-        }
+        marks = tid < per && i < i1;
+        if (marks) dv = uint32_t(dst[i]);
     }
+    auto mark = [&]() {
+        if (!marks) return;
+        if (dv >= N) {
+            atomicOr(c.status2, 2u);
+        } else {
+            const uint32_t mask = 1u << (dv % 32u);
+            if (atomicOr(&bits[dv / 32u], mask) & mask) atomicOr(c.status2, 2u);
+        }
+    };
     for (uint32_t k = tid; k < 4u * 512u; k += 256u) (&wcnt[0][0])[k] = 0u;
     const uint32_t ng = plan->n_groups;
-    if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) return;
+    if (ng > 512u || plan->n_entries != N || plan->bad > plan->n_entries) {
+        mark();
+        return;
+    }
     const int32_t sorted_signed = plan->grp_start[ng];
-    if (sorted_signed < 0 || uint32_t(sorted_signed) != N - plan->bad) return;
+    if (sorted_signed < 0 || uint32_t(sorted_signed) != N - plan->bad) {
+        mark();
+        return;
+    }
     // The entry's slot, as group_scatter_kernel computed it.
     const bool valid = id >= 0 && uint32_t(id) < E;
     const uint32_t key = valid ? uint32_t(id) : 1023u;
@@ -649,6 +662,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
         }
         if (tb + kGatherBatch * rpar > t1) break;
     }
+    mark();
 }
 
 __global__ __launch_bounds__(256) void bitset_clear_kernel(uint32_t* __restrict__ bits, uint32_t words) {
