@@ -76,14 +76,20 @@ struct TileWork {
 // tiles of those groups, in order. A group that fails the range checks contributes no
 // tiles and reports status bit 1 (it cannot occur behind a passed plan check). Returns the
 // status word read at start.
+// Small-tile enumeration (512 threads, once per workgroup): groups below wide_min entries,
+// ceil(size / 64) tiles each; s_pref[gi] = tiles of the groups before gi, s_pref[512] = all.
+// Every group field is loaded without waiting for n_groups (thread gi < 512 reads inside the
+// plan's arrays whatever n_groups holds), so the scan costs one round trip. An unusable group
+// sets status bit 1. Returns the status word read at start.
 __device__ __forceinline__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag) {
     const Plan* p = g.plan;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t ng = p->n_groups < 512u ? p->n_groups : 512u;
+    const uint32_t ng_raw = p->n_groups;
+    const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
+    const uint32_t ng = ng_raw < 512u ? ng_raw : 512u;
     uint32_t n = 0;
     if (tid < ng) {
-        const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
         if (f >= 0 && e > f && uint32_t(e) <= g.n_entries && ex >= 0 && uint32_t(ex) < g.n_experts) {
             if (uint32_t(e - f) < g.wide_min) n = (uint32_t(e - f) + 63u) / 64u;
         } else {

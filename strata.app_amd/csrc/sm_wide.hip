@@ -245,31 +245,52 @@ struct WideSmem {
 
 // Unit enumeration (512 threads, once per workgroup): groups with >= wide_min entries,
 // ceil(size / 256) units each; s_pref[gi] = units of the groups before gi, s_pref[512] = all.
-// Returns the status word read at start (bit 1: invalid plan or permutation).
-__device__ __forceinline__ uint32_t scan_wide_units(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag) {
+// With s_tiles (the routed stage kernel) the same pass also enumerates the small groups'
+// 64-row tiles as scan_small_tiles does (an unusable group sets status bit 1). Group fields
+// are loaded without waiting for n_groups (thread gi < 512 reads inside the plan's arrays), so
+// the pass costs one round trip. Returns the status word read at start.
+__device__ __forceinline__ uint32_t scan_wide_units(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag,
+                                                    uint32_t* s_tiles = nullptr, uint32_t* s_tsum = nullptr) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const Plan* p = g.plan;
     if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t ng = p->n_groups < 512u ? p->n_groups : 512u;
-    uint32_t units = 0;
+    const uint32_t ng_raw = p->n_groups;
+    const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
+    const uint32_t ng = ng_raw < 512u ? ng_raw : 512u;
+    uint32_t units = 0, tiles = 0;
     if (tid < ng) {
-        const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
-        if (f >= 0 && e > f && uint32_t(e) <= g.n_entries && ex >= 0 && uint32_t(ex) < g.n_experts &&
-            uint32_t(e - f) >= g.wide_min)
-            units = (uint32_t(e - f) + kUnitRows - 1u) / kUnitRows;
+        if (f >= 0 && e > f && uint32_t(e) <= g.n_entries && ex >= 0 && uint32_t(ex) < g.n_experts) {
+            if (uint32_t(e - f) >= g.wide_min) units = (uint32_t(e - f) + kUnitRows - 1u) / kUnitRows;
+            else tiles = (uint32_t(e - f) + 63u) / 64u;
+        } else if (s_tiles != nullptr) {
+            atomicOr(g.status, 2u);
+        }
     }
-    uint32_t incl = units;
+    uint32_t incl = units, incl_t = tiles;
 #pragma unroll
     for (uint32_t off = 1; off < 64u; off <<= 1) {
-        const uint32_t y = __shfl_up(incl, off);
-        if (lane >= off) incl += y;
+        const uint32_t y = __shfl_up(incl, off), yt = __shfl_up(incl_t, off);
+        if (lane >= off) {
+            incl += y;
+            incl_t += yt;
+        }
     }
-    if (lane == 63u) s_wsum[wave] = incl;
+    if (lane == 63u) {
+        s_wsum[wave] = incl;
+        if (s_tiles != nullptr) s_tsum[wave] = incl_t;
+    }
     __syncthreads();
-    uint32_t base = 0;
-    for (uint32_t w = 0; w < wave; ++w) base += s_wsum[w];
+    uint32_t base = 0, base_t = 0;
+    for (uint32_t w = 0; w < wave; ++w) {
+        base += s_wsum[w];
+        if (s_tiles != nullptr) base_t += s_tsum[w];
+    }
     s_pref[tid + 1] = base + incl;
     if (tid == 0) s_pref[0] = 0;
+    if (s_tiles != nullptr) {
+        s_tiles[tid + 1] = base_t + incl_t;
+        if (tid == 0) s_tiles[0] = 0;
+    }
     __syncthreads();
     return *s_flag;
 }
@@ -569,9 +590,8 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
         WideSmem w;
         TileSmem<Frag, 2> t;
     } sm;
-    __shared__ uint32_t s_pref_w[513], s_pref_t[513], s_wsum[8], s_flag, s_next_w;
-    const uint32_t flag = scan_wide_units(g, s_pref_w, s_wsum, &s_flag);
-    scan_small_tiles(g, s_pref_t, s_wsum, &s_flag);
+    __shared__ uint32_t s_pref_w[513], s_pref_t[513], s_wsum[8], s_tsum[8], s_flag, s_next_w;
+    const uint32_t flag = scan_wide_units(g, s_pref_w, s_wsum, &s_flag, s_pref_t, s_tsum);
     if (flag & 2u) {
         zero_tile_slots<MODE, 2>(g, n_ntiles, npi, n_chunks);
         return;
