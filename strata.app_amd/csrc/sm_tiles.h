@@ -76,17 +76,41 @@ struct TileWork {
 // tiles of those groups, in order. A group that fails the range checks contributes no
 // tiles and reports status bit 1 (it cannot occur behind a passed plan check). Returns the
 // status word read at start.
+// The plan's group starts and experts kept in LDS by the enumeration pass (s_grp: starts
+// [0, 513), experts [513, 1025)), so the item lookups cost no plan round trip.
+constexpr uint32_t kGrpWords = 1025;
+__device__ __forceinline__ void stash_groups(int32_t* s_grp, uint32_t tid, int32_t f, int32_t e, int32_t ex) {
+    s_grp[tid] = f;
+    if (tid == 511u) s_grp[512] = e;
+    s_grp[513u + tid] = ex;
+}
+// Start, end and expert of group gi (gi < 512): from the stash when there is one.
+__device__ __forceinline__ void group_fields(const Plan* p, const int32_t* s_grp, uint32_t gi, uint32_t& f, uint32_t& e,
+                                             uint32_t& ex) {
+    if (s_grp != nullptr) {
+        f = uint32_t(s_grp[gi]);
+        e = uint32_t(s_grp[gi + 1u]);
+        ex = uint32_t(s_grp[513u + gi]);
+    } else {
+        f = uint32_t(p->grp_start[gi]);
+        e = uint32_t(p->grp_start[gi + 1u]);
+        ex = uint32_t(p->grp_e[gi]);
+    }
+}
+
 // Small-tile enumeration (512 threads, once per workgroup): groups below wide_min entries,
 // ceil(size / 64) tiles each; s_pref[gi] = tiles of the groups before gi, s_pref[512] = all.
 // Every group field is loaded without waiting for n_groups (thread gi < 512 reads inside the
 // plan's arrays whatever n_groups holds), so the scan costs one round trip. An unusable group
 // sets status bit 1. Returns the status word read at start.
-__device__ __forceinline__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag) {
+__device__ __forceinline__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag,
+                                                     int32_t* s_grp = nullptr) {
     const Plan* p = g.plan;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t ng_raw = p->n_groups;
     const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
+    if (s_grp != nullptr) stash_groups(s_grp, tid, f, e, ex);
     const uint32_t ng = ng_raw < 512u ? ng_raw : 512u;
     uint32_t n = 0;
     if (tid < ng) {
@@ -116,7 +140,8 @@ __device__ __forceinline__ uint32_t scan_small_tiles(const RoutedGemm& g, uint32
 // effects. Uniform per workgroup.
 template <int MODE>
 __device__ __forceinline__ uint32_t staged_item_work(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item,
-                                                     uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks, TileWork& t) {
+                                                     uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks, TileWork& t,
+                                                     const int32_t* s_grp) {
     const Plan* p = g.plan;
     const uint32_t k = item / n_chunks, chunk = item - k * n_chunks;
     uint32_t lo = 0, hi = 512;
@@ -125,8 +150,8 @@ __device__ __forceinline__ uint32_t staged_item_work(const RoutedGemm& g, const 
         if (s_pref[mid] <= k) lo = mid;
         else hi = mid;
     }
-    const uint32_t f = uint32_t(p->grp_start[lo]), e = uint32_t(p->grp_start[lo + 1]);
-    const uint32_t ex = uint32_t(p->grp_e[lo]);
+    uint32_t f, e, ex;
+    group_fields(p, s_grp, lo, f, e, ex);
     t.nt_begin = chunk * npi;
     t.nt_end = t.nt_begin + npi < n_ntiles ? t.nt_begin + npi : n_ntiles;
     t.a0 = f + 64u * (k - s_pref[lo]);
@@ -141,8 +166,8 @@ __device__ __forceinline__ uint32_t staged_item_work(const RoutedGemm& g, const 
 // weights has zeroed its rows and set status bit 0 (missing) or 2 (unleased tiered slot).
 template <int MODE>
 __device__ bool staged_item(const RoutedGemm& g, const uint32_t* s_pref, uint32_t item, uint32_t n_ntiles,
-                            uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t) {
-    if (const uint32_t fault = staged_item_work<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, t)) {
+                            uint32_t npi, uint32_t n_chunks, uint32_t out_per_nt, TileWork& t, const int32_t* s_grp) {
+    if (const uint32_t fault = staged_item_work<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, t, s_grp)) {
         if (threadIdx.x == 0) atomicOr(g.status, fault);
         zero_cols<MODE>(g, t.a0, t.a1, t.nt_begin * out_per_nt, t.nt_end * out_per_nt, MODE == kDown);
         return false;
@@ -389,7 +414,7 @@ __device__ void zero_tile_slots(const RoutedGemm& g, uint32_t n_ntiles, uint32_t
 // the workgroup's column tiles, instead of being re-read from L2 for each of them.
 template <class Frag, int MODE, int NF, bool RESIDENT, bool DYNAMIC>
 __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, NF>& sm, const uint32_t* s_pref,
-                                           uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks) {
+                                           uint32_t n_ntiles, uint32_t npi, uint32_t n_chunks, const int32_t* s_grp) {
     constexpr bool dynamic = DYNAMIC;
     using S = Staged<MODE, NF>;
     using WC = WeightCopy<Frag, MODE, NF>;
@@ -423,14 +448,15 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
     const bool pf = XPF && pf_have;
     if (pf) {
         t = t_pf;
-    } else if (!staged_item<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, S::kOut, t)) {
+    } else if (!staged_item<MODE>(g, s_pref, item, n_ntiles, npi, n_chunks, S::kOut, t, s_grp)) {
         __syncthreads();  // every thread has read s_next
         if (dynamic && threadIdx.x == 0) sm.s_next = x * per + next;
         continue;
     }
     TileWork t_nx{};
     bool nx_ok = false;  // an item whose weights fault is left to its own turn
-    if (XPF && item + P < i_end) nx_ok = staged_item_work<MODE>(g, s_pref, item + P, n_ntiles, npi, n_chunks, t_nx) == 0u;
+    if (XPF && item + P < i_end)
+        nx_ok = staged_item_work<MODE>(g, s_pref, item + P, n_ntiles, npi, n_chunks, t_nx, s_grp) == 0u;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, gq = lane >> 4;
     // Read once here rather than in each epilogue, where a dependent global load would also
     // wait for the copies of the next step (visible after the first loop barrier).
@@ -624,12 +650,13 @@ __global__ __launch_bounds__(kV2Threads) void routed_gemm_staged_kernel(RoutedGe
                                                                         uint32_t n_chunks) {
     __shared__ TileSmem<Frag, NF> sm;
     __shared__ uint32_t s_pref[513], s_wsum[8], s_flag;
-    const uint32_t flag = scan_small_tiles(g, s_pref, s_wsum, &s_flag);
+    __shared__ int32_t s_grp[kGrpWords];
+    const uint32_t flag = scan_small_tiles(g, s_pref, s_wsum, &s_flag, s_grp);
     if (flag & 2u) {
         zero_tile_slots<MODE, NF>(g, n_ntiles, npi, n_chunks);
         return;
     }
-    tile_items<Frag, MODE, NF, RESIDENT, false>(g, sm, s_pref, n_ntiles, npi, n_chunks);
+    tile_items<Frag, MODE, NF, RESIDENT, false>(g, sm, s_pref, n_ntiles, npi, n_chunks, s_grp);
 }
 
 

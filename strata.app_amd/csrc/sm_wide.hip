@@ -250,12 +250,14 @@ struct WideSmem {
 // are loaded without waiting for n_groups (thread gi < 512 reads inside the plan's arrays), so
 // the pass costs one round trip. Returns the status word read at start.
 __device__ __forceinline__ uint32_t scan_wide_units(const RoutedGemm& g, uint32_t* s_pref, uint32_t* s_wsum, uint32_t* s_flag,
-                                                    uint32_t* s_tiles = nullptr, uint32_t* s_tsum = nullptr) {
+                                                    uint32_t* s_tiles = nullptr, uint32_t* s_tsum = nullptr,
+                                                    int32_t* s_grp = nullptr) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const Plan* p = g.plan;
     if (tid == 0) *s_flag = __hip_atomic_load(g.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t ng_raw = p->n_groups;
     const int32_t f = p->grp_start[tid], e = p->grp_start[tid + 1], ex = p->grp_e[tid];
+    if (s_grp != nullptr) stash_groups(s_grp, tid, f, e, ex);
     const uint32_t ng = ng_raw < 512u ? ng_raw : 512u;
     uint32_t units = 0, tiles = 0;
     if (tid < ng) {
@@ -305,7 +307,7 @@ __device__ __forceinline__ uint32_t scan_wide_units(const RoutedGemm& g, uint32_
 template <class Prod, int MODE, bool DENSE, bool DYN = false>
 __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* dw0, const uint8_t* dw1, uint32_t n_ct, uint32_t U,
                            const uint32_t* s_pref, uint8_t (&s_a)[2][kStageBytes], uint8_t (&s_b)[2][kStageBytes],
-                           int32_t* s_dst, uint32_t* s_next = nullptr) {
+                           int32_t* s_dst, uint32_t* s_next = nullptr, const int32_t* s_grp = nullptr) {
     constexpr int SB = Prod::kSlab;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const Plan* p = g.plan;
@@ -355,11 +357,12 @@ __device__ __forceinline__ void wide_items(const RoutedGemm& g, const uint8_t* d
                 if (s_pref[mid] <= uidx) lo_g = mid;
                 else hi_g = mid;
             }
-            const uint32_t f = uint32_t(p->grp_start[lo_g]), e = uint32_t(p->grp_start[lo_g + 1]);
+            uint32_t f, e, ex;
+            group_fields(p, s_grp, lo_g, f, e, ex);
             const uint32_t usz = unit_rows(e - f);
             u.a0 = f + usz * (uidx - s_pref[lo_g]);
             u.a1 = u.a0 + usz < e ? u.a0 + usz : e;
-            u.ex = uint32_t(p->grp_e[lo_g]);
+            u.ex = ex;
         }
         const uint32_t nrows = u.a1 - u.a0;
         if (!DENSE && MODE == kDown && tid < kUnitRows) s_dst[tid] = tid < nrows ? g.dst[u.a0 + tid] : -1;
@@ -591,7 +594,8 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
         TileSmem<Frag, 2> t;
     } sm;
     __shared__ uint32_t s_pref_w[513], s_pref_t[513], s_wsum[8], s_tsum[8], s_flag, s_next_w;
-    const uint32_t flag = scan_wide_units(g, s_pref_w, s_wsum, &s_flag, s_pref_t, s_tsum);
+    __shared__ int32_t s_grp[kGrpWords];
+    const uint32_t flag = scan_wide_units(g, s_pref_w, s_wsum, &s_flag, s_pref_t, s_tsum, s_grp);
     if (flag & 2u) {
         zero_tile_slots<MODE, 2>(g, n_ntiles, npi, n_chunks);
         return;
@@ -601,19 +605,20 @@ __global__ __launch_bounds__(kWideThreads) void routed_stage_kernel(RoutedGemm g
     // (per-thread constants, some of them spilled at entry) would run for nothing.
     if (MODE == kGateUp) {
         if (U > 0u) {
-            wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst);
+            wide_items<Prod, MODE, false>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b, sm.w.s_dst, nullptr,
+                                          s_grp);
             __syncthreads();  // the wide phase's LDS is free
-            tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+            tile_items<Frag, MODE, 2, RESIDENT, true>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks, s_grp);
         } else {
-            tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+            tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks, s_grp);
         }
     } else {
-        tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks);
+        tile_items<Frag, MODE, 2, RESIDENT, false>(g, sm.t, s_pref_t, n_ntiles, npi, n_chunks, s_grp);
         if (U > 0u) {
             __syncthreads();  // the tile phase's LDS is free
             // Workgroups leave the tile phase at different times: the wide items are drawn.
             wide_items<Prod, MODE, false, true>(g, nullptr, nullptr, n_ct, U, s_pref_w, sm.w.s_a, sm.w.s_b,
-                                                sm.w.s_dst, &s_next_w);
+                                                sm.w.s_dst, &s_next_w, s_grp);
         }
     }
 }
