@@ -294,6 +294,39 @@ __device__ __forceinline__ void staged_epilogue(const RoutedGemm& g, const uint3
         for (int rb = 0; rb < RB; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
 }
 
+// Gate/up with a free weight image (two images, NF = 2): the column tile's F16 rows go
+// through LDS (the image this step has finished reading, [64 rows][128 columns + 8 pad]), so
+// each wave stores 8 whole 256-byte row pieces with 16-byte stores (2 instructions) instead of
+// 16 scattered 2-byte stores. Rows past the tile's end are not stored.
+template <int RB>
+__device__ __forceinline__ void staged_epilogue_lds(const RoutedGemm& g, uint32_t a0, uint32_t a1, uint32_t col0,
+                                                    int wave, int lane, float4v (&acc)[2][4], uint8_t* stage) {
+    constexpr uint32_t kRowB = 272u;  // 128 halves + 16 bytes of pad: the 4 rows of a write hit distinct banks
+    const int n = lane & 15, gq = lane >> 4;
+    // LDS-only barriers: the next step's copies, in flight, need not land here.
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // fragments read from the image
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t row = 16u * rb + 4u * gq + i;
+            *reinterpret_cast<_Float16*>(stage + row * kRowB + 2u * (16u * wave + n)) =
+                half_sat(silu_fast(acc[0][rb][i]) * acc[1][rb][i]);
+        }
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[f][rb] = float4v{0, 0, 0, 0};
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the tile's rows are in LDS
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t row = 8u * wave + 4u * j + uint32_t(gq), a = a0 + row;
+        if (row < 16u * RB && a < a1)
+            *reinterpret_cast<u32x4*>(g.out_h + uint64_t(a) * g.n_out + col0 + 8u * n) =
+                *reinterpret_cast<const u32x4*>(stage + row * kRowB + 16u * n);
+    }
+}
+
 // Bytes moved per lane by one LDS-DMA copy of weight-row slabs: 16 where the slab size
 // allows, else 4 (Q2_K's 84-byte slabs). Lane l of a copy writes at LDS base + l * size.
 template <int SB> struct ChunkBytes { static constexpr int value = SB % 16 == 0 ? 16 : 4; };
@@ -623,8 +656,12 @@ __device__ __forceinline__ void tile_items(const RoutedGemm& g, TileSmem<Frag, N
 #pragma unroll
             for (int f = 0; f < NF; ++f) c[f].prepare();
             slab_mma<Frag, NF, RB>(sa[RESIDENT ? sb : par], n, gq, c, acc, [](int) {});
-            if (sb == n_slabs - 1u)  // column tile complete
-                staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
+            if (sb == n_slabs - 1u) {  // column tile complete
+                if constexpr (MODE == kGateUp && NF == 2 && WBUF == 2)
+                    staged_epilogue_lds<RB>(g, t.a0, t.a1, nt * S::kOut, wave, lane, acc, sw[par]);
+                else
+                    staged_epilogue<MODE, NF, RB>(g, s_dst, t.a0, t.a1, nt * S::kOut, wave, n, gq, acc);
+            }
             cur_sb = nx_sb;
             cur_nt = nx_nt - t.nt_begin;
         }
