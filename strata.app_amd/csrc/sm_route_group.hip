@@ -315,9 +315,23 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
         const uint32_t per = (n_tiles + 31u) / 32u;
         const uint32_t t_begin = slice * per < n_tiles ? slice * per : n_tiles;
         const uint32_t t_end = t_begin + per < n_tiles ? t_begin + per : n_tiles;
+        // Up to kScanHeld counts per thread are loaded at once and kept for the rewrite (one
+        // round trip, where a load after each store would cost one per tile).
+        constexpr uint32_t kScanHeld = 16;
+        const bool held = per <= kScanHeld;
+        uint32_t hv[kScanHeld];
         uint32_t local = 0;
-        if (e < E)
-            for (uint32_t t = t_begin; t < t_end; ++t) local += hist[uint64_t(t) * E + e];
+        if (e < E) {
+            if (held) {
+#pragma unroll
+                for (uint32_t j = 0; j < kScanHeld; ++j)
+                    hv[j] = t_begin + j < t_end ? hist[uint64_t(t_begin + j) * E + e] : 0u;
+#pragma unroll
+                for (uint32_t j = 0; j < kScanHeld; ++j) local += hv[j];
+            } else {
+                for (uint32_t t = t_begin; t < t_end; ++t) local += hist[uint64_t(t) * E + e];
+            }
+        }
         part[slice][el] = local;
         __syncthreads();
         if (e < E) {
@@ -328,11 +342,20 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_plan_kernel(uint32_t*
             if (slice == 31u)
                 __hip_atomic_store(&hist[uint64_t(n_tiles) * E + e], run + local, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-            for (uint32_t t = t_begin; t < t_end; ++t) {
-                const uint64_t h = uint64_t(t) * E + e;
-                const uint32_t c = hist[h];
-                hist[h] = run;
-                run += c;
+            if (held) {
+#pragma unroll
+                for (uint32_t j = 0; j < kScanHeld; ++j)
+                    if (t_begin + j < t_end) {
+                        hist[uint64_t(t_begin + j) * E + e] = run;
+                        run += hv[j];
+                    }
+            } else {
+                for (uint32_t t = t_begin; t < t_end; ++t) {
+                    const uint64_t h = uint64_t(t) * E + e;
+                    const uint32_t c = hist[h];
+                    hist[h] = run;
+                    run += c;
+                }
             }
         }
     }
