@@ -58,6 +58,19 @@ def test_route_topk_bit_exact(moe, orc, gpu_ctx, stream, T, E, K, divide):
 @pytest.mark.parametrize("T", [1, 7, 25, 26, 64, 300, 4096])
 @pytest.mark.parametrize("pattern", rp.PATTERNS)
 def test_grouping_gather_bit_exact(moe, orc, gpu_ctx, stream, pattern, T, E):
+    _check_grouping_gather(moe, orc, gpu_ctx, stream, pattern, T, E)
+
+
+# The scan keeps up to 16 of its 256-entry tiles per thread in registers (512 tiles: N = 131072
+# entries); longer columns take its re-reading loop. 13107 tokens x 10 is 512 tiles, 16384 x 10
+# is 640.
+@pytest.mark.parametrize("T", [13107, 16384])
+@pytest.mark.parametrize("pattern", ["mixed", "invalid_ids"])
+def test_grouping_gather_long_columns(moe, orc, gpu_ctx, stream, pattern, T):
+    _check_grouping_gather(moe, orc, gpu_ctx, stream, pattern, T, 512)
+
+
+def _check_grouping_gather(moe, orc, gpu_ctx, stream, pattern, T, E):
     import torch
     print(f"case grouping pattern={pattern} T={T} E={E}", flush=True)
     K, d = 10, 256
