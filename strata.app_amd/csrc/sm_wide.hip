@@ -104,11 +104,10 @@ struct ProdQ80 {
     uint32_t w8, sh;
     __device__ __forceinline__ void load(const uint8_t* sb, uint32_t g, uint32_t b) {
         const uint8_t* p = sb + 68u * g + 32u * b;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // dword reads: blocks are only 4-byte aligned
-            wa[i] = ld_global<uint32_t>(p + 4 * i);
-            wb[i] = ld_global<uint32_t>(p + 16 + 4 * i);
-        }
+        // 16-byte loads at 4-byte-aligned addresses (allowed on this part): three loads per
+        // lane instead of nine dword loads, each one cache access per lane.
+        wa = ld_global<u32x4>(p);
+        wb = ld_global<u32x4>(p + 16);
         w8 = ld_global<uint32_t>(p + 32);
         sh = 16u * b;
     }
@@ -141,9 +140,9 @@ struct ProdQ2K {
         g = grp;
         b = bb;
         const uint32_t n = grp >> 1, jbase = 2u * (grp & 1u);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)  // dword reads: slabs are only 4-byte aligned
-            qs[i] = ld_global<uint32_t>(sb + 16 + 32 * n + 16 * bb + 4 * i);
+        // One 16-byte load at a 4-byte-aligned address (unaligned vector loads are allowed on
+        // this part), not four dword loads: each is one cache access per lane.
+        qs = ld_global<u32x4>(sb + 16 + 32 * n + 16 * bb);
         sc = ld_global<uint32_t>(sb + 8 * n + 2 * jbase);
         dd = ld_global<uint32_t>(sb + 80);
     }
